@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""Speculative-decoding throughput on one MI355X.
+
+Workload (default `--config cfg4`, BASELINE configs[3], the metric's
+"d24+d4, bs32"): target d24 (D 1536, 12 heads of 128, 12 KV heads, vocab
+65536, max_seq_len 2048, SSSL with short window 1024), draft = 4 layers
+sharing the target's layers 0-3 and wte / lm_head; random-init N(0, 0.02)
+weights drawn on the device (seed 2), bf16 weights / KV cache with fp32
+accumulation; batch 32, prompts of 1024 uniform random ids, 512 new tokens,
+draft_steps 6, temperature 0.8 rejection sampling, Philox seed 2, no top-k.
+
+A "step" is one speculative round for the whole batch (k draft steps,
+the (k+1)-token verify, accept/reject, bookkeeping, one host sync). Prompt
+prefill and `--warmup` rounds are untimed; then `--steps` rounds (0 = until
+every row has its max_tokens) are timed between two synchronisations.
+value = tokens emitted in the timed rounds (accepted drafts + corrections +
+bonus tokens, counted up to max_tokens per row) / timed seconds.
+
+roofline: the verify-pass attention (split-KV flash-decode, the dominant
+HBM consumer) timed with HIP events on the engine's stream, at the state the
+timed run ends in, over one S (window 1024) and one L (full) layer weighted
+18:6 like the d24 SSSL stack. Algorithmic bytes per launch = the distinct
+visible K and V bytes of every row (read once) + Q + O.
+
+cpu_baseline: the CPU restatement of the reference algorithm (oracle/,
+literal mode: token-by-token verify and full re-prefill on rejection) on
+the same architecture with the same weights, batch 1, on a bounded sample.
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+CONFIGS = {
+    # name: (target cfg kwargs, draft layers, batch, prompt, new, k, temperature, seed)
+    "cfg2": (dict(sequence_len=2048, vocab_size=65536, n_layer=12, n_head=6, n_kv_head=6, n_embd=768,
+                  window_pattern="SSSL", short_window=1024), 2, 1, 512, 256, 4, 0.0, 0),
+    "cfg4": (dict(sequence_len=2048, vocab_size=65536, n_layer=24, n_head=12, n_kv_head=12, n_embd=1536,
+                  window_pattern="SSSL", short_window=1024), 4, 32, 1024, 512, 6, 0.8, 2),
+    "cfg5": (dict(sequence_len=8192, vocab_size=65536, n_layer=24, n_head=12, n_kv_head=4, n_embd=1536,
+                  window_pattern="SSSL", short_window=2048), 4, 128, 6144, 1024, 8, 0.0, 3),
+}
+HBM_PEAK_GBS = 8000.0
+
+
+def attention_roofline(sess, n_iter=20):
+    """Time the verify attention at the session's current lengths."""
+    import torch
+    from flaxchat_amd import _lib
+    T = sess.T
+    B, k = sess.B, sess.k
+    W = k + 1
+    dev = T.device
+    s = sess.stream
+    t_len = sess.bufs["t_len"].cpu().numpy().astype(np.int64)
+    q = torch.randn(B, W, T.H, T.hd, device=dev).to(torch.bfloat16)
+    y = torch.empty_like(q)
+    start = sess.bufs["t_len"].clone()
+    nvalid = torch.full((B,), W, dtype=torch.int32, device=dev)
+    cap = sess.tcache.cap
+    res = {}
+    es = 2
+    layer_elems = B * T.G * cap * T.hd
+    for name, layer in (("S", 0), ("L", T.L - 1)):
+        win = T.windows[layer]
+        max_keys = min(cap, win + W) if win > 0 else cap
+        nb = _lib.lib().fc_attention_workspace_bytes(B, W, T.H, T.G, T.hd, max_keys)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+        kp = sess.tcache.k.data_ptr() + layer * layer_elems * es
+        vp = sess.tcache.v.data_ptr() + layer * layer_elems * es
+        def launch():
+            _lib.check(_lib.lib().fc_attention(q.data_ptr(), kp, vp, y.data_ptr(), B, W, T.H, T.G, T.hd, cap,
+                                               start.data_ptr(), nvalid.data_ptr(), win, max_keys, 1,
+                                               ws.data_ptr(), ws.numel(), s.cuda_stream), "attention")
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                launch()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(n_iter):
+                launch()
+            e1.record(s)
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / n_iter
+        # distinct visible keys per row: full layer 0..pos_last; window layer
+        # from max(0, pos_first - window) to pos_last
+        pos_last = t_len + W - 1
+        lo = np.maximum(0, t_len - win) if win > 0 else np.zeros_like(t_len)
+        keys = (pos_last - lo + 1).sum()
+        kv_bytes = keys * T.G * T.hd * 2 * es
+        qo_bytes = 2 * B * W * T.H * T.hd * es
+        res[name] = dict(ms=ms, bytes=int(kv_bytes + qo_bytes))
+    nS = sum(1 for w in T.windows if w > 0 and w < T.config.sequence_len)
+    nL = T.L - nS
+    tot_b = nS * res["S"]["bytes"] + nL * res["L"]["bytes"]
+    tot_s = (nS * res["S"]["ms"] + nL * res["L"]["ms"]) / 1e3
+    return dict(achieved=tot_b / tot_s / 1e9, per_launch_bytes=tot_b / T.L, per_launch_us=tot_s / T.L * 1e6,
+                S=res["S"], L=res["L"], nS=nS, nL=nL)
+
+
+def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0):
+    """The oracle's literal-mode generate_speculative on host cores."""
+    from flaxchat_amd.runtime import to_host
+    from oracle.spec import spec_literal
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        cores = 1
+    ht = to_host(dm_t)
+    hd = to_host(dm_d)
+    V = dm_t.V
+    prompt = np.random.default_rng(seed).integers(0, V, 16).tolist()
+    new = 6
+    t0 = time.perf_counter()
+    out = spec_literal(ht, hd, prompt, max_tokens=new, temperature=temperature, top_k=None, seed=seed,
+                       draft_steps=k)
+    dt = time.perf_counter() - t0
+    return {"value": round((len(out) - len(prompt)) / dt, 4), "unit": "tokens/s", "cores": int(cores),
+            "kind": "port",
+            "sample": f"oracle spec_literal (restatement of flaxchat/engine.py:410-608, fp32 numpy) on the "
+                      f"{cfg_name} architecture and weights, batch 1, prompt 16 ids (not the full prompt), "
+                      f"{new} new tokens, k={k}, T={temperature}, including prefill; {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=0, help="timed rounds (0 = until every row is done)")
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="cfg4", choices=sorted(CONFIGS))
+    ap.add_argument("--top-k", type=int, default=0)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; the speculative engine shards over the batch "
+              "(one full replica per GPU, no collective in the decode loop), which is not built here.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.engine import SpecSession
+    from flaxchat_amd.runtime import DeviceModel
+
+    tk, n_draft, B, P, new, k, temp, seed = CONFIGS[args.config]
+    cfg = GPTConfig(**tk)
+    t_init = time.perf_counter()
+    target = DeviceModel.random_init(cfg, seed=seed, dtype="bf16")
+    draft = target.make_draft(n_draft)
+    prompts = np.random.default_rng(seed).integers(0, cfg.vocab_size, (B, P)).tolist()
+    sess = SpecSession(target, draft, prompts, new, temp, args.top_k or None, seed, k, use_graph=not args.no_graph)
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter()
+    sess.prefill()
+    sess.stream.synchronize()
+    prefill_s = time.perf_counter() - t_pre
+    print(f"[bench] init {t_pre - t_init:.1f}s prefill {prefill_s:.2f}s ({B}x{P} tokens)", file=sys.stderr, flush=True)
+    if args.warmup:
+        sess.run(max_rounds=args.warmup)
+    done_before = sess.emitted_tokens()
+    rounds_before = sess.rounds
+    sess.stream.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sess.run(max_rounds=args.steps or None)
+    sess.stream.synchronize()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    steps = sess.rounds - rounds_before
+    toks = sess.emitted_tokens() - done_before
+    acc = np.concatenate(sess.accept_hist) if sess.accept_hist else np.zeros(1)
+    print(f"[bench] {steps} rounds {toks} tokens {el:.3f}s mean accepted/round {acc.mean():.2f}",
+          file=sys.stderr, flush=True)
+
+    roof = None
+    if not args.no_roofline:
+        r = attention_roofline(sess)
+        roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_attn_mfma + k_attn_combine (verify, k+1 queries per row)",
+                "per_launch_bytes": int(r["per_launch_bytes"]), "per_launch_us": round(r["per_launch_us"], 2),
+                "S_layer": r["S"], "L_layer": r["L"]}
+        print(f"[bench] verify attention {r['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(target, draft, args.config, seed, k, temp)
+    out = {
+        "metric": "spec-decode accepted tokens/s (d24+d4, bs32); verify-attn % HBM peak",
+        "value": round(toks / el, 2), "unit": "tokens/s", "n_gpus": 1, "steps": int(steps),
+        "warmup": int(args.warmup), "ms_per_step": round(el / max(steps, 1) * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform random prompt ids, random-init N(0,0.02) weights)",
+        "config": {"workload": f"{args.config}: d{cfg.n_layer}+d{n_draft} D{cfg.n_embd} H{cfg.n_head} "
+                               f"G{cfg.n_kv_head} V{cfg.vocab_size}, batch {B}, prompt {P}, {new} new, "
+                               f"k={k}, T={temp}, top_k={args.top_k or None}, Philox seed {seed}",
+                   "global_batch": B, "seq_len": P + new, "parallelism": "single GPU",
+                   "graph": not args.no_graph},
+        "mean_accepted_per_round": round(float(acc.mean()), 3),
+        "prefill_s": round(prefill_s, 3),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

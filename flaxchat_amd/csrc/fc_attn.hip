@@ -1,0 +1,458 @@
+// Per-token attention prologue and split-KV flash-decode attention.
+//
+// Prologue (flaxchat/engine.py:96-126, flaxchat/gpt.py:65-71): value
+// embedding gate on the V heads, RoPE (base 100000) and 1.2 * RMSNorm on
+// the Q and K heads, then the K/V append at each valid slot's position.
+//
+// Attention (flaxchat/engine.py:128-156): for query position p and KV
+// group g = h / (H / G), softmax over keys j with j <= p and, for layers
+// with a window W > 0, p - j <= W (W + 1 keys, inclusive). The reference
+// scores every cached position and masks with -1e9; the masked terms are
+// exact zeros in fp32, so reading only the visible keys is the same sum.
+//
+// bf16 path (head_dim 128): one workgroup per (row, KV group, query block of
+// 16 columns, key split). Columns are (slot, head-in-group) pairs, so a
+// verify chunk's k+1 tokens and the GQA heads of a group share every K/V
+// tile read. Each wave walks 32-key tiles with two matrix-core products:
+//   S^T = K Q^T   (16 keys x 16 columns per MFMA; two MFMAs per tile, with
+//                  the key rows interleaved so each lane ends up holding 8
+//                  consecutive keys of its column), then online softmax in
+//                  registers with wave shuffles,
+//   O^T += V^T P^T (P taken straight from registers as the B operand; V^T
+//                  read from the 32-key blocked-transposed V cache as one
+//                  16-byte load per lane).
+// The four waves merge in LDS; splits merge in k_attn_combine.
+// fp32 path (parity mode, or head_dim != 128): one workgroup per query with
+// the reference's operation order (scores, max, exp, normalise, weighted sum).
+#include "fc_common.h"
+#include "fc_internal.h"
+
+// ---------------------------------------------------------------------------
+// Prologue: one wave per (token row m, head slot hh in [0, H + 2G)).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv, const T* __restrict__ h,
+                                                  const int* __restrict__ tokens, const float* __restrict__ rcos,
+                                                  const float* __restrict__ rsin, int rope_len,
+                                                  const T* __restrict__ ve, const float* __restrict__ ve_gate,
+                                                  int D, T* __restrict__ kc, T* __restrict__ vc, int B, int W, int H,
+                                                  int G, int hd, int cap, const int* __restrict__ start,
+                                                  const int* __restrict__ nvalid, T* __restrict__ q) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int NH = H + 2 * G;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  if (item >= (int64_t)B * W * NH) return;
+  const int m = (int)(item / NH), hh = (int)(item % NH);
+  const int b = m / W, slot = m - b * W;
+  const int n = nvalid[b];
+  const bool valid = slot >= W - n;
+  const int pos = start[b] + slot - (W - n);
+  const int half = hd >> 1;
+  const bool act = lane < half;
+  const float* row = qkv + ((int64_t)m * NH + hh) * hd;
+  float x1 = act ? row[lane] : 0.f, x2 = act ? row[lane + half] : 0.f;
+  if (hh < H + G) {
+    const int pc = min(max(pos, 0), rope_len - 1);
+    const float c = act ? rcos[(int64_t)pc * half + lane] : 0.f;
+    const float s = act ? rsin[(int64_t)pc * half + lane] : 0.f;
+    float y1 = x1 * c + x2 * s;
+    float y2 = x1 * (-s) + x2 * c;
+    const float ss = wave_sum(y1 * y1 + y2 * y2);
+    const float inv = 1.f / sqrtf(ss / (float)hd + 1e-6f);
+    y1 = y1 * inv * 1.2f;
+    y2 = y2 * inv * 1.2f;
+    if (hh < H) {
+      if (act) {
+        T* qo = q + ((int64_t)m * H + hh) * hd;
+        st<T>(qo, lane, valid ? y1 : 0.f);
+        st<T>(qo, lane + half, valid ? y2 : 0.f);
+      }
+    } else if (valid && act && pos < cap) {
+      const int g = hh - H;
+      T* ko = kc + (((int64_t)b * G + g) * cap + pos) * hd;
+      st<T>(ko, lane, y1);
+      st<T>(ko, lane + half, y2);
+    }
+  } else {
+    const int g = hh - H - G;
+    if (ve != nullptr) {
+      float part = lane < 12 ? ld<T>(h, (int64_t)m * D + lane) * ve_gate[g * 12 + lane] : 0.f;
+      const float z = wave_sum(part);
+      const float gate = 3.f * (1.f / (1.f + expf(-z)));
+      const int tok = tokens[m];
+      if (act) {
+        const T* vr = ve + ((int64_t)tok * G + g) * hd;
+        x1 = x1 + gate * ld<T>(vr, lane);
+        x2 = x2 + gate * ld<T>(vr, lane + half);
+      }
+    }
+    if (valid && act && pos < cap) {
+      T* vb = vc + ((((int64_t)b * G + g) * (cap / 32) + pos / 32) * hd) * 32;
+      st<T>(vb, (int64_t)lane * 32 + (pos & 31), x1);
+      st<T>(vb, (int64_t)(lane + half) * 32 + (pos & 31), x2);
+    }
+  }
+}
+
+int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const fc_model* m, int layer,
+                       const fc_cache* c, const int* start, const int* nvalid, int B, int W, void* q,
+                       hipStream_t s) {
+  const fc_layer& L = m->layers[layer];
+  const int H = m->n_head, G = m->n_kv_head, hd = m->head_dim;
+  FC_CHECK_ARG(hd <= 128 && hd % 2 == 0, "head_dim must be even and <= 128");
+  const int64_t layer_elems = (int64_t)c->batch * G * c->cap * hd;
+  const int64_t items = (int64_t)B * W * (H + 2 * G);
+  const dim3 grid((unsigned)((items + 3) / 4));
+  if (m->dtype == FC_BF16) {
+    bf16_t* kc = (bf16_t*)c->k + layer_elems * layer;
+    bf16_t* vc = (bf16_t*)c->v + layer_elems * layer;
+    hipLaunchKernelGGL(k_prologue<bf16_t>, grid, dim3(256), 0, s, qkv, (const bf16_t*)h, tokens, m->rope_cos,
+                       m->rope_sin, m->rope_len, (const bf16_t*)L.ve, L.ve_gate, m->n_embd, kc, vc, B, W, H, G, hd,
+                       c->cap, start, nvalid, (bf16_t*)q);
+  } else {
+    float* kc = (float*)c->k + layer_elems * layer;
+    float* vc = (float*)c->v + layer_elems * layer;
+    hipLaunchKernelGGL(k_prologue<float>, grid, dim3(256), 0, s, qkv, (const float*)h, tokens, m->rope_cos,
+                       m->rope_sin, m->rope_len, (const float*)L.ve, L.ve_gate, m->n_embd, kc, vc, B, W, H, G, hd,
+                       c->cap, start, nvalid, (float*)q);
+  }
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 MFMA split-KV attention (head_dim 128)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma16a(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+}
+__device__ __forceinline__ uint32_t pack2bf(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+                                                   const bf16_t* __restrict__ vc, float* __restrict__ part_o,
+                                                   float* __restrict__ part_ml, int W, int H, int G, int cap,
+                                                   const int* __restrict__ start, const int* __restrict__ nvalid,
+                                                   int window, int split_keys, int nsplit, int nqblk,
+                                                   float scale_log2) {
+  constexpr int HD = 128;
+  const int split = blockIdx.x, qb = blockIdx.y, bg = blockIdx.z;
+  const int b = bg / G, g = bg - b * G, rep = H / G;
+  const int n = nvalid[b], s0 = start[b], off = W - n;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, g4 = lane >> 4;
+  const int ncol = W * rep;
+  const int64_t pidx = ((int64_t)bg * nqblk + qb) * nsplit + split;
+
+  // key range of the whole query block
+  const int f = max(qb * 16, off * rep), lcol = min(qb * 16 + 15, ncol - 1);
+  int kbeg = 0, kend = 0;
+  if (f <= lcol) {
+    const int pf = s0 + f / rep - off, pl = s0 + lcol / rep - off;
+    const int klo = window > 0 ? max(0, pf - window) : 0;
+    const int khi = min(pl + 1, cap);
+    kbeg = klo + split * split_keys;
+    kend = min(khi, kbeg + split_keys);
+  }
+  if (kbeg >= kend) {
+    if (threadIdx.x < 16) {
+      part_ml[(pidx * 16 + threadIdx.x) * 2 + 0] = -INFINITY;
+      part_ml[(pidx * 16 + threadIdx.x) * 2 + 1] = 0.f;
+    }
+    return;
+  }
+  // this lane's query column
+  const int col = qb * 16 + c;
+  const int j = col / rep, head = g * rep + (col - j * rep);
+  const bool cvalid = col < ncol && j >= off;
+  const int pos_c = s0 + j - off;
+  const int lo_c = window > 0 ? max(0, pos_c - window) : 0;
+
+  const uint4 zero = {0u, 0u, 0u, 0u};
+  uint4 qf[4];
+  {
+    const bf16_t* qr = q + (((int64_t)b * W + (cvalid ? j : 0)) * H + head) * HD + 8 * g4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = cvalid ? *(const uint4*)(qr + 32 * s) : zero;
+  }
+  const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
+  const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
+  const int r = c;
+  const int krow0 = 8 * (r >> 2) + (r & 3);
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 O[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int t0 = kbeg & ~31;
+  const int ntiles = (kend - t0 + 31) >> 5;
+  for (int t = wave; t < ntiles; t += 4) {
+    const int kb = t0 + 32 * t;
+    uint4 kf[2][4];
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const bf16_t* kr = kbase + (int64_t)(kb + krow0 + 4 * cc) * HD + 8 * g4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[cc][s] = *(const uint4*)(kr + 32 * s);
+    }
+    uint4 vf[8];
+    const bf16_t* vt = vbase + (int64_t)(kb >> 5) * HD * 32 + r * 32 + 8 * g4;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) vf[db] = *(const uint4*)(vt + db * 16 * 32);
+
+    f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sc[cc] = mfma16a(kf[cc][s], qf[s], sc[cc]);
+    float p[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int jj = i + 4 * cc;
+        const int key = kb + 8 * g4 + jj;
+        const bool ok = cvalid && key >= kbeg && key < kend && key >= lo_c && key <= pos_c;
+        p[jj] = ok ? sc[cc][i] * scale_log2 : -INFINITY;
+        mt = fmaxf(mt, p[jj]);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+    const float m_new = fmaxf(m_run, mt);
+    float alpha = 1.f, psum = 0.f;
+    if (m_new == -INFINITY) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) p[jj] = 0.f;
+    } else {
+      alpha = exp2f(m_run - m_new);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        p[jj] = exp2f(p[jj] - m_new);
+        psum += p[jj];
+      }
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    uint4 pf;
+    pf.x = pack2bf(p[0], p[1]);
+    pf.y = pack2bf(p[2], p[3]);
+    pf.z = pack2bf(p[4], p[5]);
+    pf.w = pack2bf(p[6], p[7]);
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      O[db] *= alpha;
+      O[db] = mfma16a(vf[db], pf, O[db]);
+    }
+  }
+  // merge the four waves
+  float l_tot = l_run + __shfl_xor(l_run, 16, WAVE);
+  l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
+  __shared__ float sm[4][16], sl[4][16];
+  __shared__ float so[4][16][HD + 4];
+  if (g4 == 0) {
+    sm[wave][c] = m_run;
+    sl[wave][c] = l_tot;
+  }
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[wave][c][16 * db + 4 * g4 + i] = O[db][i];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 16 * HD; idx += 256) {
+    const int qc = idx / HD, d = idx - qc * HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][qc]);
+    float o = 0.f, L = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a = exp2f(sm[w][qc] - M);
+        o += a * so[w][qc][d];
+        L += a * sl[w][qc];
+      }
+    }
+    part_o[(pidx * 16 + qc) * HD + d] = o;
+    if (d == 0) {
+      part_ml[(pidx * 16 + qc) * 2 + 0] = M;
+      part_ml[(pidx * 16 + qc) * 2 + 1] = L;
+    }
+  }
+}
+
+// one wave per (token row, head): merge the key splits and normalise
+template <typename T>
+__global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
+                                                      const float* __restrict__ part_ml, T* __restrict__ y, int B,
+                                                      int W, int H, int G, int nqblk, int nsplit,
+                                                      const int* __restrict__ nvalid) {
+  constexpr int HD = 128;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  if (item >= (int64_t)B * W * H) return;
+  const int m = (int)(item / H), h = (int)(item % H);
+  const int b = m / W, j = m - b * W;
+  const int rep = H / G, g = h / rep;
+  T* yo = y + ((int64_t)m * H + h) * HD;
+  if (j < W - nvalid[b]) {
+    st<T>(yo, lane, 0.f);
+    st<T>(yo, lane + 64, 0.f);
+    return;
+  }
+  const int col = j * rep + (h - g * rep), qb = col >> 4, c = col & 15;
+  const int64_t base = ((int64_t)(b * G + g) * nqblk + qb) * nsplit;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[((base + s) * 16 + c) * 2]);
+  float o0 = 0.f, o1 = 0.f, L = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = part_ml[((base + s) * 16 + c) * 2];
+      if (ms == -INFINITY) continue;
+      const float a = exp2f(ms - M);
+      L += a * part_ml[((base + s) * 16 + c) * 2 + 1];
+      const float* po = part_o + ((base + s) * 16 + c) * HD;
+      o0 += a * po[lane];
+      o1 += a * po[lane + 64];
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  st<T>(yo, lane, o0 * inv);
+  st<T>(yo, lane + 64, o1 * inv);
+}
+
+// ---------------------------------------------------------------------------
+// VALU attention, reference operation order (fp32 parity path, any hd <= 128)
+// ---------------------------------------------------------------------------
+#define VALU_MAXK 8192
+template <typename T>
+__global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, const T* __restrict__ kc,
+                                                   const T* __restrict__ vc, T* __restrict__ y, int W, int H, int G,
+                                                   int hd, int cap, const int* __restrict__ start,
+                                                   const int* __restrict__ nvalid, int window, float scale) {
+  __shared__ float qs[128];
+  __shared__ float sc[VALU_MAXK];
+  __shared__ float red[16];
+  const int m = blockIdx.x / H, h = blockIdx.x - (blockIdx.x / H) * H;
+  const int b = m / W, j = m - b * W;
+  const int n = nvalid[b], off = W - n;
+  const int rep = H / G, g = h / rep;
+  T* yo = y + ((int64_t)m * H + h) * hd;
+  if (j < off) {
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) st<T>(yo, d, 0.f);
+    return;
+  }
+  const int pos = min(start[b] + j - off, cap - 1);
+  const int lo = window > 0 ? max(0, pos - window) : 0;
+  const int nk = min(pos - lo + 1, VALU_MAXK);
+  const int64_t bg = (int64_t)b * G + g;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = ld<T>(q, ((int64_t)m * H + h) * hd + d);
+  __syncthreads();
+  for (int i = threadIdx.x; i < nk; i += blockDim.x) {
+    const T* kr = kc + (bg * cap + lo + i) * hd;
+    float s = 0.f;
+    for (int d = 0; d < hd; ++d) s += qs[d] * ld<T>(kr, d);
+    sc[i] = s * scale;
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < nk; i += blockDim.x) mx = fmaxf(mx, sc[i]);
+  mx = block_max(mx, red);
+  float sum = 0.f;
+  for (int i = threadIdx.x; i < nk; i += blockDim.x) {
+    const float e = expf(sc[i] - mx);
+    sc[i] = e;
+    sum += e;
+  }
+  sum = block_sum(sum, red);
+  for (int i = threadIdx.x; i < nk; i += blockDim.x) sc[i] = sc[i] / sum;
+  __syncthreads();
+  const T* vb = vc + bg * (cap / 32) * hd * 32;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float acc = 0.f;
+    for (int i = 0; i < nk; ++i) {
+      const int key = lo + i;
+      acc += sc[i] * ld<T>(vb, ((int64_t)(key >> 5) * hd + d) * 32 + (key & 31));
+    }
+    st<T>(yo, d, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+AttnGrid fc_attn_grid(int batch, int W, int n_head, int n_kv_head, int max_keys) {
+  AttnGrid a;
+  const int rep = n_head / n_kv_head;
+  a.nqblk = (W * rep + 15) / 16;
+  const int64_t units = (int64_t)batch * n_kv_head * a.nqblk;
+  const int range = max(max_keys, 1);
+  int want = (int)((1024 + units - 1) / units);
+  want = max(1, min(want, (range + 127) / 128));
+  int sk = (range + want - 1) / want;
+  sk = max(128, (sk + 127) / 128 * 128);
+  a.split_keys = sk;
+  a.nsplit = (range + sk - 1) / sk;
+  return a;
+}
+
+int64_t fc_attn_part_bytes(int batch, int W, int n_head, int n_kv_head, int head_dim, int max_keys) {
+  if (head_dim != 128) return 0;
+  AttnGrid a = fc_attn_grid(batch, W, n_head, n_kv_head, max_keys);
+  const int64_t units = (int64_t)batch * n_kv_head * a.nqblk * a.nsplit * 16;
+  return fc_align(units * 128 * 4) + fc_align(units * 2 * 4);
+}
+
+int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int W, int H, int G, int hd,
+                        int cap, const int* start, const int* nvalid, int window, int max_keys, int dtype,
+                        void* part, int64_t part_bytes, hipStream_t s) {
+  FC_CHECK_ARG(H % G == 0, "n_head must be a multiple of n_kv_head");
+  FC_CHECK_ARG(cap % 32 == 0, "cache capacity must be a multiple of 32");
+  const float scale = 1.f / sqrtf((float)hd);
+  if (dtype == FC_BF16 && hd == 128) {
+    AttnGrid a = fc_attn_grid(B, W, H, G, max_keys);
+    const int64_t units = (int64_t)B * G * a.nqblk * a.nsplit * 16;
+    FC_CHECK_ARG(part != nullptr && part_bytes >= fc_align(units * 128 * 4) + fc_align(units * 2 * 4),
+                 "attention workspace too small");
+    float* po = (float*)part;
+    float* pml = (float*)((char*)part + fc_align(units * 128 * 4));
+    hipLaunchKernelGGL(k_attn_mfma, dim3(a.nsplit, a.nqblk, B * G), dim3(256), 0, s, (const bf16_t*)q,
+                       (const bf16_t*)kc, (const bf16_t*)vc, po, pml, W, H, G, cap, start, nvalid, window,
+                       a.split_keys, a.nsplit, a.nqblk, scale * 1.4426950408889634f);
+    FC_LAUNCH_CHECK();
+    const int64_t items = (int64_t)B * W * H;
+    hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, po, pml,
+                       (bf16_t*)y, B, W, H, G, a.nqblk, a.nsplit, nvalid);
+  } else {
+    FC_CHECK_ARG(hd <= 128, "head_dim must be <= 128");
+    FC_CHECK_ARG(max_keys <= VALU_MAXK, "VALU attention supports at most 8192 visible keys");
+    const unsigned blocks = (unsigned)(B * W * H);
+    if (dtype == FC_BF16)
+      hipLaunchKernelGGL(k_attn_valu<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)q, (const bf16_t*)kc,
+                         (const bf16_t*)vc, (bf16_t*)y, W, H, G, hd, cap, start, nvalid, window, scale);
+    else
+      hipLaunchKernelGGL(k_attn_valu<float>, dim3(blocks), dim3(256), 0, s, (const float*)q, (const float*)kc,
+                         (const float*)vc, (float*)y, W, H, G, hd, cap, start, nvalid, window, scale);
+  }
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int64_t fc_attention_workspace_bytes(int32_t batch, int32_t W, int32_t n_head, int32_t n_kv_head,
+                                                int32_t head_dim, int32_t max_keys) {
+  return fc_attn_part_bytes(batch, W, n_head, n_kv_head, head_dim, max_keys);
+}
+
+extern "C" int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y, int32_t batch, int32_t W,
+                                int32_t n_head, int32_t n_kv_head, int32_t head_dim, int32_t cap,
+                                const int32_t* start, const int32_t* nvalid, int32_t window, int32_t max_keys,
+                                int32_t dtype, void* work, int64_t work_bytes, void* stream) {
+  FC_CHECK_ARG(q && kc && vc && y && start && nvalid, "null pointer");
+  FC_CHECK_ARG(batch > 0 && W > 0 && n_head > 0 && n_kv_head > 0, "sizes");
+  FC_CHECK_ARG(max_keys > 0 && max_keys <= cap, "max_keys must be in [1, cap]");
+  return fc_launch_attention(q, kc, vc, y, batch, W, n_head, n_kv_head, head_dim, cap, start, nvalid, window,
+                             max_keys, dtype, work, work_bytes, (hipStream_t)stream);
+}

@@ -1,0 +1,35 @@
+// Internal (not exported) declarations shared by the .hip translation units.
+#pragma once
+#include "fc_common.h"
+
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_RELU2 = 2, EPI_MLPOUT = 3, EPI_SOFTCAP = 4 };
+
+struct Epi {
+  int mode;
+  int out_dtype;
+  void* out;
+  int64_t ldo;
+  // EPI_MLPOUT: out is x (fp32, in place)
+  const float* x0;
+  float* xb;
+  float r, a, lb;
+  int capture, last;
+  // EPI_SOFTCAP: output row m -> (m / n_out) * row_stride + (m % n_out) * V
+  int n_out;
+  int64_t row_stride;
+  int V;
+};
+
+int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, hipStream_t s);
+
+struct AttnGrid {
+  int nqblk, nsplit, split_keys;
+};
+AttnGrid fc_attn_grid(int batch, int W, int n_head, int n_kv_head, int max_keys);
+int64_t fc_attn_part_bytes(int batch, int W, int n_head, int n_kv_head, int head_dim, int max_keys);
+int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int W, int H, int G, int hd,
+                        int cap, const int* start, const int* nvalid, int window, int max_keys, int dtype,
+                        void* part, int64_t part_bytes, hipStream_t s);
+int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const fc_model* m, int layer,
+                       const fc_cache* c, const int* start, const int* nvalid, int B, int W, void* q, hipStream_t s);
+int fc_launch_row_stats(const float* logits, int rows, int V, float T, int top_k, fc_rowstat* stats, hipStream_t s);

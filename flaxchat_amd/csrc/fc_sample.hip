@@ -1,0 +1,579 @@
+// Vocab-wide sampling, accept/reject and the device-side round bookkeeping.
+//
+// Restates flaxchat/engine.py:461-482 (top-k filter, probabilities,
+// categorical draw), :525-592 (accept / reject / residual / bonus) and
+// replaces the full re-prefill of :593-606 by length-pointer rollback.
+//
+// Random stream: Philox4x32-10, key = seed, counter = (element / 4, row,
+// round, slot); slots: draft sample i -> i, accept uniform i -> 16 + i,
+// rejection draw -> 48, bonus draw -> 49 (generate_fast: round = step, slot 0).
+// A categorical draw is Gumbel-max over log(max(p, 1e-10)), the same method
+// as jax.random.categorical on the reference's log(max(p, 1e-10)) input.
+#include "fc_common.h"
+#include "fc_internal.h"
+#include <mutex>
+
+#define SLOT_ACCEPT 16
+#define SLOT_REJECT 48
+#define SLOT_BONUS 49
+#define NTHR 1024
+#define BIG_POS 0x3fffffff
+
+// ---------------------------------------------------------------------------
+// error plumbing, version, graphs
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+void fc_set_error(const std::string& s) { g_err = s; }
+extern "C" const char* fc_last_error(void) { return g_err.c_str(); }
+extern "C" int32_t fc_version(void) { return 100; }
+
+extern "C" int32_t fc_graph_begin(void* stream) {
+  FC_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+  return FC_OK;
+}
+extern "C" int32_t fc_graph_end(void* stream, void** exec_out) {
+  FC_CHECK_ARG(exec_out, "exec_out");
+  hipGraph_t g = nullptr;
+  FC_HIP(hipStreamEndCapture((hipStream_t)stream, &g));
+  hipGraphExec_t ex = nullptr;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    fc_set_error(std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    return FC_ERR_HIP;
+  }
+  *exec_out = (void*)ex;
+  return FC_OK;
+}
+extern "C" int32_t fc_graph_launch(void* exec, void* stream) {
+  FC_CHECK_ARG(exec, "exec");
+  FC_HIP(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream));
+  return FC_OK;
+}
+extern "C" int32_t fc_graph_destroy(void* exec) {
+  if (exec) FC_HIP(hipGraphExecDestroy((hipGraphExec_t)exec));
+  return FC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Row statistics (block of NTHR threads per row)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t mono(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float unmono(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+__device__ __forceinline__ bool kept(float z, int idx, uint32_t tau_key, int tie_idx) {
+  const uint32_t k = mono(z);
+  return k > tau_key || (k == tau_key && idx <= tie_idx);
+}
+
+struct StatSmem {
+  unsigned hist[256];
+  float redv[16];
+  int redi[16];
+  unsigned cnt[NTHR];
+  int sel, remaining, cnt_eq, tie_idx;
+  fc_rowstat res;  // the row's statistics, for the block's own use
+};
+
+// lax.top_k keep-set (exactly k entries; larger value first, lower index
+// first among equal values) by 8-bit radix select over order-preserving
+// keys, then max / normaliser of z/T over the kept set and the argmax.
+__device__ void row_stats_block(const float* __restrict__ z, int V, float T, int top_k, fc_rowstat* out,
+                                StatSmem& sm) {
+  const int tid = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < V; i += NTHR) argmax_merge(bv, bi, z[i], i);
+  block_argmax(bv, bi, sm.redv, sm.redi);
+  const int amax = bi;
+  uint32_t tau_key = mono(-INFINITY);
+  int tie_idx = V;
+  if (T > 0.f && top_k > 0 && top_k < V) {
+    uint32_t prefix = 0, maskbits = 0;
+    if (tid == 0) sm.remaining = top_k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += NTHR) sm.hist[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < V; i += NTHR) {
+        const uint32_t k = mono(z[i]);
+        if ((k & maskbits) == prefix) atomicAdd(&sm.hist[(k >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        unsigned cum = 0;
+        int rem = sm.remaining;
+        for (int d = 255; d >= 0; --d) {
+          const unsigned h = sm.hist[d];
+          if (cum + h >= (unsigned)rem) {
+            sm.sel = d;
+            sm.remaining = rem - (int)cum;
+            sm.cnt_eq = (int)h;
+            break;
+          }
+          cum += h;
+        }
+      }
+      __syncthreads();
+      prefix |= ((uint32_t)sm.sel) << shift;
+      maskbits |= 0xffu << shift;
+    }
+    tau_key = prefix;
+    const int need = sm.remaining, cnt_eq = sm.cnt_eq;
+    if (need < cnt_eq) {
+      // index of the need-th entry equal to tau, in index order
+      const int chunk = (V + NTHR - 1) / NTHR;
+      const int lo = tid * chunk, hi = min(V, lo + chunk);
+      unsigned c = 0;
+      for (int i = lo; i < hi; ++i) c += mono(z[i]) == tau_key;
+      sm.cnt[tid] = c;
+      __syncthreads();
+      if (tid == 0) {
+        unsigned acc = 0;
+        for (int t = 0; t < NTHR; ++t) {
+          const unsigned v = sm.cnt[t];
+          sm.cnt[t] = acc;
+          acc += v;
+        }
+      }
+      __syncthreads();
+      const unsigned before = sm.cnt[tid];
+      if (before < (unsigned)need && before + c >= (unsigned)need) {
+        unsigned k = before;
+        for (int i = lo; i < hi; ++i)
+          if (mono(z[i]) == tau_key && ++k == (unsigned)need) {
+            sm.tie_idx = i;
+            break;
+          }
+      }
+      __syncthreads();
+      tie_idx = sm.tie_idx;
+    }
+  }
+  float mx = 0.f, sum = 1.f;
+  if (T > 0.f) {
+    float m = -INFINITY;
+    for (int i = tid; i < V; i += NTHR)
+      if (kept(z[i], i, tau_key, tie_idx)) m = fmaxf(m, z[i] / T);
+    mx = block_max(m, sm.redv);
+    float s = 0.f;
+    for (int i = tid; i < V; i += NTHR)
+      if (kept(z[i], i, tau_key, tie_idx)) s += expf(z[i] / T - mx);
+    sum = block_sum(s, sm.redv);
+  }
+  if (tid == 0) {
+    fc_rowstat r{};
+    r.mx = mx;
+    r.sum = sum;
+    r.tau = unmono(tau_key);
+    r.tie_idx = tie_idx;
+    r.argmax = amax;
+    sm.res = r;
+    if (out) *out = r;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ float prob_at(const float* z, const fc_rowstat& rs, float T, int i) {
+  return kept(z[i], i, mono(rs.tau), rs.tie_idx) ? expf(z[i] / T - rs.mx) / rs.sum : 0.f;
+}
+
+__device__ __forceinline__ float gumbel_of(uint32_t bits) { return -logf(-logf(u_open(bits))); }
+
+// Gumbel-max draw over V entries; mode 0: p, mode 1: residual max(0, p - q)
+// renormalised (falls back to p when its mass is zero).
+__device__ int block_draw(const float* __restrict__ zp, const fc_rowstat& sp, const float* __restrict__ zq,
+                          const fc_rowstat& sq, int mode, float T, int V, uint64_t seed, int row, int rnd,
+                          int slot, StatSmem& sm) {
+  const int tid = threadIdx.x;
+  float rsum = 0.f;
+  if (mode == 1) {
+    float s = 0.f;
+    for (int i = tid; i < V; i += NTHR) s += fmaxf(prob_at(zp, sp, T, i) - prob_at(zq, sq, T, i), 0.f);
+    rsum = block_sum(s, sm.redv);
+    if (!(rsum > 0.f)) mode = 0;
+  }
+  const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const int ngrp = (V + 3) >> 2;
+  for (int gi = tid; gi < ngrp; gi += NTHR) {
+    const u32x4 r = philox4x32_10(u32x4{(uint32_t)gi, (uint32_t)row, (uint32_t)rnd, (uint32_t)slot}, k0, k1);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int i = gi * 4 + w;
+      if (i >= V) break;
+      float p = prob_at(zp, sp, T, i);
+      if (mode == 1) p = fmaxf(p - prob_at(zq, sq, T, i), 0.f) / rsum;
+      const float sc = logf(fmaxf(p, 1e-10f)) + gumbel_of(pick(r, w));
+      argmax_merge(bv, bi, sc, i);
+    }
+  }
+  block_argmax(bv, bi, sm.redv, sm.redi);
+  return bi;
+}
+
+__global__ __launch_bounds__(NTHR) void k_row_stats(const float* __restrict__ logits, int V, float T, int top_k,
+                                                    fc_rowstat* __restrict__ stats) {
+  __shared__ StatSmem sm;
+  row_stats_block(logits + (int64_t)blockIdx.x * V, V, T, top_k, stats + blockIdx.x, sm);
+}
+
+int fc_launch_row_stats(const float* logits, int rows, int V, float T, int top_k, fc_rowstat* stats, hipStream_t s) {
+  if (rows <= 0) return FC_OK;
+  hipLaunchKernelGGL(k_row_stats, dim3(rows), dim3(NTHR), 0, s, logits, V, T, top_k, stats);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int32_t fc_row_stats(const float* logits, int32_t rows, int32_t V, float temperature, int32_t top_k,
+                                fc_rowstat* stats, void* stream) {
+  FC_CHECK_ARG(logits && stats && V > 0, "arguments");
+  return fc_launch_row_stats(logits, rows, V, temperature, top_k, stats, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Speculative round kernels
+// ---------------------------------------------------------------------------
+struct SpecDev {  // the fc_spec_state fields the kernels read, by value
+  int B, k, max_tokens, gen_cap, V;
+  float T;
+  int top_k;
+  uint64_t seed;
+  int *t_len, *d_len, *t_pend, *d_pend, *t_pend_n, *d_pend_n, *t_dirty, *d_dirty, *gen, *gen_n, *prompt_len,
+      *round, *result;
+  int *tok_d0, *n_d0, *start_d, *tok_ds, *ones, *tok_v, *start_v, *n_v, *drafts;
+  float *q_logits, *p_logits;
+  fc_rowstat *q_stats, *p_stats;
+};
+
+static SpecDev to_dev(const fc_spec_state* s) {
+  SpecDev d;
+  d.B = s->batch; d.k = s->k; d.max_tokens = s->max_tokens; d.gen_cap = s->gen_cap; d.V = s->vocab;
+  d.T = s->temperature; d.top_k = s->top_k; d.seed = s->seed;
+  d.t_len = s->t_len; d.d_len = s->d_len; d.t_pend = s->t_pend; d.d_pend = s->d_pend;
+  d.t_pend_n = s->t_pend_n; d.d_pend_n = s->d_pend_n; d.t_dirty = s->t_dirty; d.d_dirty = s->d_dirty;
+  d.gen = s->gen; d.gen_n = s->gen_n; d.prompt_len = s->prompt_len; d.round = s->round; d.result = s->result;
+  d.tok_d0 = s->tok_d0; d.n_d0 = s->n_d0; d.start_d = s->start_d; d.tok_ds = s->tok_ds; d.ones = s->ones;
+  d.tok_v = s->tok_v; d.start_v = s->start_v; d.n_v = s->n_v; d.drafts = s->drafts;
+  d.q_logits = s->q_logits; d.p_logits = s->p_logits; d.q_stats = s->q_stats; d.p_stats = s->p_stats;
+  return d;
+}
+
+// Round plan: chunk descriptors for draft step 0 (pending draft tokens,
+// right-aligned in 2 slots), draft steps 1..k-1 and the verify chunk
+// (pending target token + k drafts).
+__global__ void k_spec_plan(SpecDev s) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= s.B) return;
+  const int dn = s.d_pend_n[b];
+  s.tok_d0[b * 2 + 0] = dn == 2 ? s.d_pend[b * 2 + 0] : 0;
+  s.tok_d0[b * 2 + 1] = s.d_pend[b * 2 + dn - 1];
+  s.n_d0[b] = dn;
+  const int dl = s.d_len[b];
+  s.start_d[b] = dl;
+  for (int i = 1; i < s.k; ++i) s.start_d[i * s.B + b] = dl + dn + i - 1;
+  s.ones[b] = 1;
+  s.tok_v[b * (s.k + 1)] = s.t_pend[b * 2];
+  s.start_v[b] = s.t_len[b];
+  s.n_v[b] = s.t_pend_n[b] + s.k;
+}
+
+// Draft step i: statistics of the draft logits row, proposal d_{i+1}
+// (flaxchat/engine.py:493-499), written where the next chunks read it.
+__global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i) {
+  __shared__ StatSmem sm;
+  __shared__ int tok_s;
+  const int b = blockIdx.x;
+  const float* z = s.q_logits + ((int64_t)b * s.k + i) * s.V;
+  fc_rowstat* rs = s.q_stats + b * s.k + i;
+  row_stats_block(z, s.V, s.T, s.top_k, rs, sm);
+  int tok;
+  const fc_rowstat st = sm.res;
+  if (s.T > 0.f) tok = block_draw(z, st, z, st, 0, s.T, s.V, s.seed, b, s.round[b], i, sm);
+  else tok = st.argmax;
+  if (threadIdx.x == 0) {
+    tok_s = tok;
+    s.drafts[b * s.k + i] = tok;
+    s.tok_v[b * (s.k + 1) + 1 + i] = tok;
+    if (i + 1 < s.k) s.tok_ds[(i + 1) * s.B + b] = tok;
+  }
+}
+
+// Accept/reject (flaxchat/engine.py:525-592) and the rollback bookkeeping.
+__global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
+  __shared__ StatSmem sm;
+  __shared__ int sh_mode, sh_row, sh_n, sh_acc, sh_rej, sh_bonus, sh_kp;
+  __shared__ int emitted[64];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int K = s.k, V = s.V;
+  const bool greedy = !(s.T > 0.f);
+  int* res = s.result + (int64_t)b * FC_RES_STRIDE;
+  if (tid == 0) {
+    const int ng = s.gen_n[b] - s.prompt_len[b];
+    const int kp = min(K, s.max_tokens - ng);
+    sh_kp = kp;
+    sh_mode = -1;
+    sh_n = 0;
+    sh_acc = 0;
+    sh_rej = -1;
+    sh_bonus = 0;
+    if (kp > 0) {
+      sh_mode = 0;
+      int acc = 0, n = 0;
+      for (int i = 0; i < kp; ++i) {
+        const int dt = s.drafts[b * K + i];
+        const fc_rowstat ps = s.p_stats[b * (K + 1) + i];
+        if (greedy) {
+          const int am = ps.argmax;
+          emitted[n++] = am == dt ? dt : am;
+          ++acc;
+          if (am != dt) { sh_rej = i; break; }
+        } else {
+          const fc_rowstat qs = s.q_stats[b * K + i];
+          const float* zp = s.p_logits + ((int64_t)b * (K + 1) + i) * V;
+          const float* zq = s.q_logits + ((int64_t)b * K + i) * V;
+          const float pm = prob_at(zp, ps, s.T, dt);
+          const float pd = prob_at(zq, qs, s.T, dt);
+          if (pd == 0.f) {
+            sh_mode = 1; sh_row = i; ++acc; sh_rej = i;
+            break;
+          }
+          const double ap = fmin(1.0, (double)pm / (double)pd);
+          const u32x4 r = philox4x32_10(u32x4{0u, (uint32_t)b, (uint32_t)s.round[b], (uint32_t)(SLOT_ACCEPT + i)},
+                                        (uint32_t)s.seed, (uint32_t)(s.seed >> 32));
+          const double u = (double)u_half(r.x);
+          if (u < ap) {
+            emitted[n++] = dt;
+            ++acc;
+          } else {
+            sh_mode = 2; sh_row = i; ++acc; sh_rej = i;
+            break;
+          }
+        }
+      }
+      sh_n = n;
+      sh_acc = acc;
+      sh_bonus = acc == kp;
+    }
+  }
+  __syncthreads();
+  if (sh_mode < 0) {
+    if (tid == 0) {
+      res[0] = 0; res[1] = 0; res[2] = -1; res[3] = 4; res[4] = 0;
+      s.round[b] += 1;
+    }
+    return;
+  }
+  const int rnd = s.round[b];
+  if (sh_mode > 0) {
+    const int i = sh_row;
+    const fc_rowstat ps = s.p_stats[b * (K + 1) + i];
+    const fc_rowstat qs = s.q_stats[b * K + i];
+    const int c = block_draw(s.p_logits + ((int64_t)b * (K + 1) + i) * V, ps, s.q_logits + ((int64_t)b * K + i) * V,
+                             qs, sh_mode == 2 ? 1 : 0, s.T, V, s.seed, b, rnd, SLOT_REJECT, sm);
+    if (tid == 0) emitted[sh_n++] = c;
+    __syncthreads();
+  }
+  const int kp = sh_kp;
+  if (sh_bonus) {
+    const fc_rowstat ps = s.p_stats[b * (K + 1) + kp];
+    int bt;
+    if (greedy) bt = ps.argmax;
+    else bt = block_draw(s.p_logits + ((int64_t)b * (K + 1) + kp) * V, ps, nullptr, ps, 0, s.T, V, s.seed, b, rnd,
+                         SLOT_BONUS, sm);
+    if (tid == 0) emitted[sh_n++] = bt;
+    __syncthreads();
+  }
+  if (tid != 0) return;
+  // ---- bookkeeping (the rollback state machine) ----
+  const int n_emit = sh_n;
+  const int G0 = s.gen_n[b];
+  int* gen = s.gen + (int64_t)b * s.gen_cap;
+  int flags = 0;
+  for (int i = 0; i < n_emit; ++i)
+    if (G0 + i < s.gen_cap) gen[G0 + i] = emitted[i];
+  const int gn = min(G0 + n_emit, s.gen_cap);
+  s.gen_n[b] = gn;
+  const int tb = s.t_len[b], npt = s.t_pend_n[b], db = s.d_len[b], npd = s.d_pend_n[b];
+  if (sh_bonus) {
+    const int bonus = emitted[n_emit - 1];
+    s.t_len[b] = tb + npt + kp;
+    s.t_pend[b * 2] = bonus;
+    s.t_pend_n[b] = 1;
+    if (kp == K) {
+      s.d_len[b] = db + npd + K - 1;
+      s.d_pend[b * 2] = s.drafts[b * K + K - 1];
+      s.d_pend[b * 2 + 1] = bonus;
+      s.d_pend_n[b] = 2;
+    } else {
+      s.d_len[b] = db + npd + kp;
+      s.d_pend[b * 2] = bonus;
+      s.d_pend_n[b] = 1;
+    }
+    if (sh_rej >= 0) {  // rejected last draft: caches keep it, output has the correction
+      const int pos = G0 + kp - 1;
+      s.t_dirty[b] = min(s.t_dirty[b], pos);
+      s.d_dirty[b] = min(s.d_dirty[b], pos);
+    }
+  } else {
+    const int a = sh_acc;
+    const int t_new = min(s.t_dirty[b], tb + npt + a - 1);
+    const int d_new = min(s.d_dirty[b], db + npd + a - 1);
+    s.t_len[b] = t_new;
+    s.d_len[b] = d_new;
+    s.t_dirty[b] = BIG_POS;
+    s.d_dirty[b] = BIG_POS;
+    s.t_pend[b * 2] = gen[gn - 1];
+    s.t_pend_n[b] = 1;
+    if (gn - t_new != 1) flags |= 1;  // host feeds gen[t_new, gn-1) then sets t_len = gn-1
+    const int dp = gn - d_new;
+    if (dp == 2) {
+      s.d_pend[b * 2] = gen[gn - 2];
+      s.d_pend[b * 2 + 1] = gen[gn - 1];
+      s.d_pend_n[b] = 2;
+    } else {
+      s.d_pend[b * 2] = gen[gn - 1];
+      s.d_pend_n[b] = 1;
+      if (dp != 1) flags |= 2;
+    }
+  }
+  if (gn - s.prompt_len[b] >= s.max_tokens) flags |= 4;
+  s.round[b] = rnd + 1;
+  res[0] = n_emit;
+  res[1] = sh_acc;
+  res[2] = sh_rej;
+  res[3] = flags;
+  res[4] = kp;
+  for (int i = 0; i < n_emit && i < FC_RES_STRIDE - 8; ++i) res[8 + i] = emitted[i];
+}
+
+static int check_spec(const fc_spec_state* st) {
+  FC_CHECK_ARG(st && st->batch > 0 && st->k > 0 && st->k <= 16 && st->vocab > 0, "spec state sizes (k in 1..16)");
+  FC_CHECK_ARG(st->t_len && st->d_len && st->gen && st->gen_n && st->result && st->q_logits && st->p_logits &&
+                   st->q_stats && st->p_stats && st->drafts && st->tok_v && st->tok_ds && st->tok_d0,
+               "spec state pointers");
+  return FC_OK;
+}
+
+extern "C" int32_t fc_spec_accept(const fc_spec_state* st, void* stream) {
+  int rc = check_spec(st);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  SpecDev d = to_dev(st);
+  rc = fc_launch_row_stats(st->p_logits, st->batch * (st->k + 1), st->vocab, st->temperature, st->top_k,
+                           st->p_stats, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_accept, dim3(st->batch), dim3(NTHR), 0, s, d);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache, const fc_model* draft,
+                                 const fc_cache* dcache, const fc_spec_state* st, void* work, int64_t work_bytes,
+                                 void* stream) {
+  int rc = check_spec(st);
+  if (rc) return rc;
+  FC_CHECK_ARG(target && draft && tcache && dcache, "models / caches");
+  FC_CHECK_ARG(target->vocab == draft->vocab && target->vocab == st->vocab, "main and draft vocab differ");
+  FC_CHECK_ARG(tcache->batch == st->batch && dcache->batch == st->batch, "batch");
+  hipStream_t s = (hipStream_t)stream;
+  SpecDev d = to_dev(st);
+  const int B = st->batch, K = st->k, V = st->vocab;
+  hipLaunchKernelGGL(k_spec_plan, dim3((B + 255) / 256), dim3(256), 0, s, d);
+  FC_LAUNCH_CHECK();
+  for (int i = 0; i < K; ++i) {
+    fc_chunk ch{};
+    if (i == 0) {
+      ch.W = 2;
+      ch.tokens = st->tok_d0;
+      ch.start = st->start_d;
+      ch.nvalid = st->n_d0;
+    } else {
+      ch.W = 1;
+      ch.tokens = st->tok_ds + (int64_t)i * B;
+      ch.start = st->start_d + (int64_t)i * B;
+      ch.nvalid = st->ones;
+    }
+    ch.n_out = 1;
+    ch.logits = st->q_logits + (int64_t)i * V;
+    ch.logits_stride = (int64_t)K * V;
+    rc = fc_forward(draft, dcache, &ch, work, work_bytes, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i);
+    FC_LAUNCH_CHECK();
+  }
+  fc_chunk vch{};
+  vch.W = K + 1;
+  vch.tokens = st->tok_v;
+  vch.start = st->start_v;
+  vch.nvalid = st->n_v;
+  vch.n_out = K + 1;
+  vch.logits = st->p_logits;
+  vch.logits_stride = (int64_t)(K + 1) * V;
+  rc = fc_forward(target, tcache, &vch, work, work_bytes, stream);
+  if (rc) return rc;
+  return fc_spec_accept(st, stream);
+}
+
+// ---------------------------------------------------------------------------
+// generate_fast sampling step (flaxchat/engine.py:308-324, 343-368)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTHR) void k_fast_sample(const float* __restrict__ logits, int V, float T, int top_k,
+                                                      uint64_t seed, int eos, int* __restrict__ gen, int gen_cap,
+                                                      int* __restrict__ pos, int* __restrict__ done,
+                                                      int* __restrict__ step, const int* __restrict__ max_pos,
+                                                      int* __restrict__ tok_cur, fc_rowstat* __restrict__ stats) {
+  __shared__ StatSmem sm;
+  const int b = blockIdx.x;
+  if (done[b] || pos[b] >= max_pos[b]) return;
+  const float* z = logits + (int64_t)b * V;
+  row_stats_block(z, V, T, top_k, stats + b, sm);
+  int tok;
+  const fc_rowstat rs = sm.res;
+  if (T > 0.f) {
+    const uint32_t tk = mono(rs.tau);
+    const int rnd = step[b];
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    const int ngrp = (V + 3) >> 2;
+    for (int gi = threadIdx.x; gi < ngrp; gi += NTHR) {
+      const u32x4 r = philox4x32_10(u32x4{(uint32_t)gi, (uint32_t)b, (uint32_t)rnd, 0u}, (uint32_t)seed,
+                                    (uint32_t)(seed >> 32));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int i = gi * 4 + w;
+        if (i >= V) break;
+        if (!kept(z[i], i, tk, rs.tie_idx)) continue;
+        argmax_merge(bv, bi, z[i] / T + gumbel_of(pick(r, w)), i);
+      }
+    }
+    block_argmax(bv, bi, sm.redv, sm.redi);
+    tok = bi;
+  } else {
+    tok = rs.argmax;
+  }
+  if (threadIdx.x == 0) {
+    const int p = pos[b] + 1;
+    if (p < gen_cap) gen[(int64_t)b * gen_cap + p] = tok;
+    pos[b] = p;
+    tok_cur[b] = tok;
+    step[b] += 1;
+    if (tok == eos) done[b] = 1;
+  }
+}
+
+extern "C" int32_t fc_fast_sample(const float* logits, int32_t batch, int32_t V, float temperature, int32_t top_k,
+                                  uint64_t seed, int32_t eos, int32_t* gen, int32_t gen_cap, int32_t* pos,
+                                  int32_t* done, int32_t* step, const int32_t* max_pos, int32_t* tok_cur,
+                                  fc_rowstat* stats, void* stream) {
+  FC_CHECK_ARG(logits && gen && pos && done && step && max_pos && tok_cur && stats, "null pointer");
+  FC_CHECK_ARG(batch > 0 && V > 0 && gen_cap > 0, "sizes");
+  hipLaunchKernelGGL(k_fast_sample, dim3(batch), dim3(NTHR), 0, (hipStream_t)stream, logits, V, temperature, top_k,
+                     seed, eos, gen, gen_cap, pos, done, step, max_pos, tok_cur, stats);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}

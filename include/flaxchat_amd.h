@@ -1,0 +1,204 @@
+/*
+ * flaxchat_amd: C-ABI of the MI355X (gfx950) speculative-decoding engine.
+ *
+ * Every entry point takes plain device pointers and sizes, enqueues work on
+ * the HIP stream it is given (`stream` is a hipStream_t; NULL = the null
+ * stream), allocates nothing, and returns FC_OK (0) or a negative status;
+ * fc_last_error() then describes the failure. No C++ exception crosses the
+ * boundary. The caller owns every buffer.
+ *
+ * The reference (mlnomadpy/flaxchat) has no native code: each entry point
+ * below replaces a piece of eager JAX in flaxchat/engine.py or
+ * flaxchat/gpt.py, cited on its declaration. The Python host
+ * (flaxchat_amd/engine.py) keeps the reference's call surface,
+ * generate_speculative() and generate_fast(), on top of this ABI.
+ *
+ * Layouts (row-major, C order):
+ *   Linear weights   [out][in]   (the transpose of Flax's (in, out) kernel)
+ *   K cache          [layer][batch][kv_head][cap][head_dim]
+ *   V cache          [layer][batch][kv_head][cap/32][head_dim][32]
+ *                    (32-position blocks stored transposed so that the
+ *                    P·V matrix-core operand is one 16-byte load per lane)
+ *   smear history    [batch][cap][n_embd] fp32 (smeared embedding per position)
+ *   chunk tokens     [batch][W], valid slots right-aligned: slot j of row b
+ *                    is valid iff j >= W - nvalid[b]; its position is
+ *                    start[b] + j - (W - nvalid[b]).
+ */
+#ifndef FLAXCHAT_AMD_H
+#define FLAXCHAT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FC_OK 0
+#define FC_ERR_ARG (-1)
+#define FC_ERR_HIP (-2)
+#define FC_ERR_UNSUPPORTED (-3)
+#define FC_ERR_CAPACITY (-4)
+
+#define FC_F32 0
+#define FC_BF16 1
+
+/* One transformer block's parameters (flaxchat/gpt.py:85-99, 154-163). */
+typedef struct fc_layer {
+  const void* wqkv;      /* [(H+2G)*hd][D]  c_q | c_k | c_v stacked on out   */
+  const void* wo;        /* [D][H*hd]       attn.c_proj                       */
+  const void* wfc;       /* [4D][D]         mlp.c_fc                          */
+  const void* wproj;     /* [D][4D]         mlp.c_proj                        */
+  const void* ve;        /* [Vp][G*hd] value embedding, NULL if none          */
+  const float* ve_gate;  /* [G][12] fp32, NULL if none                        */
+  int32_t window;        /* left window (> 0) or 0 for none                   */
+  float resid_lambda;    /* resid_lambdas[i]                                  */
+  float x0_lambda;       /* x0_lambdas[i]                                     */
+} fc_layer;
+
+/* A model (flaxchat/gpt.py:202-261). `layers` is a HOST array. */
+typedef struct fc_model {
+  int32_t n_layer, n_embd, n_head, n_kv_head, head_dim, vocab, vocab_pad, dtype;
+  const void* wte;        /* [Vp][D]                                          */
+  const void* lm_head;    /* [Vp][D] (== wte when tied)                       */
+  const float* smear_gate;/* [24]                                             */
+  float smear_lambda, backout_lambda;
+  const float* rope_cos;  /* [rope_len][hd/2] fp32                            */
+  const float* rope_sin;
+  int32_t rope_len;
+  const fc_layer* layers;
+} fc_model;
+
+/* Preallocated KV cache + smear history of one model. */
+typedef struct fc_cache {
+  void* k;
+  void* v;
+  float* hist;
+  int32_t batch, cap;     /* cap is a multiple of 32                          */
+} fc_cache;
+
+/* One chunk of tokens per row, fed at per-row positions. */
+typedef struct fc_chunk {
+  int32_t W;
+  const int32_t* tokens;  /* [B][W]  device                                   */
+  const int32_t* start;   /* [B]     device                                   */
+  const int32_t* nvalid;  /* [B]     device                                   */
+  int32_t n_out;          /* logits for the last n_out slots of each row      */
+  float* logits;          /* row (b, r) at logits + b*logits_stride + r*V     */
+  int64_t logits_stride;  /* floats between rows b and b+1                    */
+} fc_chunk;
+
+/* Per-row sampling statistics of a logits row (see fc_row_stats). */
+typedef struct fc_rowstat {
+  float mx;        /* max over kept entries of z/T                           */
+  float sum;       /* sum over kept entries of exp(z/T - mx)                 */
+  float tau;       /* top-k threshold value (-inf when top-k is off)         */
+  int32_t tie_idx; /* entries equal to tau are kept iff index <= tie_idx     */
+  int32_t argmax;  /* first index of the maximum                             */
+  int32_t pad[3];
+} fc_rowstat;
+
+/* Device state of a speculative-decoding batch (one row per sequence).
+ * All pointers are device int32 arrays sized as noted; the host fills
+ * them once after prefill and then only reads `result` and `gen`. */
+typedef struct fc_spec_state {
+  int32_t batch, k, max_tokens, gen_cap, vocab;
+  float temperature;      /* <= 0: greedy                                      */
+  int32_t top_k;          /* <= 0: off                                         */
+  uint64_t seed;
+  int32_t* t_len;  int32_t* d_len;       /* [B] cache lengths                  */
+  int32_t* t_pend; int32_t* d_pend;      /* [B][2] pending tokens              */
+  int32_t* t_pend_n; int32_t* d_pend_n;  /* [B]                                */
+  int32_t* t_dirty; int32_t* d_dirty;    /* [B] earliest fed != emitted pos    */
+  int32_t* gen;    int32_t* gen_n;       /* [B][gen_cap] tokens incl. prompt   */
+  int32_t* prompt_len;                   /* [B]                                */
+  int32_t* round;                        /* [B] round counter (Philox)         */
+  int32_t* result;                       /* [B][FC_RES_STRIDE]                 */
+  /* per-round scratch */
+  int32_t* tok_d0;   /* [B][2]          draft chunk 0 tokens                   */
+  int32_t* n_d0;     /* [B]                                                    */
+  int32_t* start_d;  /* [k][B]          draft step start positions             */
+  int32_t* tok_ds;   /* [k][B]          draft step tokens (steps 1..k-1)       */
+  int32_t* ones;     /* [B]             all 1                                  */
+  int32_t* tok_v;    /* [B][k+1]        verify chunk tokens                    */
+  int32_t* start_v;  /* [B]                                                    */
+  int32_t* n_v;      /* [B]                                                    */
+  int32_t* drafts;   /* [B][k]                                                 */
+  float* q_logits;   /* [B][k][V]                                              */
+  float* p_logits;   /* [B][k+1][V]                                            */
+  fc_rowstat* q_stats; /* [B][k]                                               */
+  fc_rowstat* p_stats; /* [B][k+1]                                             */
+} fc_spec_state;
+
+#define FC_RES_STRIDE 40
+/* result row layout: [0] n_emitted this round, [1] accepted, [2] rejected
+ * index or -1, [3] flags (bit0 target needs catch-up, bit1 draft needs
+ * catch-up, bit2 row finished), [4] k', [8..8+k+1] emitted tokens. */
+
+const char* fc_last_error(void);
+int32_t fc_version(void);
+
+/* Bytes of workspace fc_forward needs for `batch` rows of W slots. */
+int64_t fc_forward_workspace_bytes(const fc_model* m, int32_t batch, int32_t W, int32_t n_out);
+
+/* Feed one chunk through the model: embedding + smear, every block, head.
+ * Replaces the per-token `_single_step_forward` (flaxchat/engine.py:51-177)
+ * and the token-by-token `_prefill` (flaxchat/engine.py:396-407) with one
+ * batched multi-token pass; appends K/V at each valid slot's position. */
+int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chunk* ch,
+                   void* work, int64_t work_bytes, void* stream);
+
+/* GEMM with fused epilogue: out[M][N] = epi(A[M][K] . W[N][K]^T), A and W in
+ * `dtype`. Replaces the nnx.Linear matmuls of flaxchat/engine.py:106-108,
+ * 158, 161, 172 (flaxchat/gpt.py:93-99, 154-163). epi: 0 store fp32,
+ * 1 add into fp32 out, 2 relu^2 (flaxchat/gpt.py:161) stored in `dtype`,
+ * 4 15*tanh(z/15) softcap (flaxchat/engine.py:173-174) stored fp32. */
+int32_t fc_gemm(const void* A, const void* W, void* out, int32_t M, int32_t N, int32_t K,
+                int32_t dtype, int32_t epi, void* stream);
+
+/* Split-KV flash-decode attention over a cache layer (flaxchat/engine.py:128-156):
+ * GQA head grouping, causal + inclusive sliding window `pos - j <= window`.
+ * q: [B][W][H][hd] dtype; y: [B][W][H*hd] dtype. */
+int64_t fc_attention_workspace_bytes(int32_t batch, int32_t W, int32_t n_head, int32_t n_kv_head,
+                                     int32_t head_dim, int32_t max_keys);
+int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y,
+                     int32_t batch, int32_t W, int32_t n_head, int32_t n_kv_head, int32_t head_dim,
+                     int32_t cap, const int32_t* start, const int32_t* nvalid, int32_t window,
+                     int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes, void* stream);
+
+/* Per-row statistics of fp32 logits rows (flaxchat/engine.py:461-476):
+ * lax.top_k keep-set (exactly k, lower index first among ties), max and
+ * softmax normaliser of z/T over it, and the first-index argmax. */
+int32_t fc_row_stats(const float* logits, int32_t rows, int32_t V, float temperature,
+                     int32_t top_k, fc_rowstat* stats, void* stream);
+
+/* One speculative round on device (flaxchat/engine.py:484-606 with the
+ * sequential verify replaced by one (k+1)-token verify chunk and the
+ * re-prefill replaced by length-pointer rollback): draft k steps,
+ * verify, accept/reject with residual resampling, bonus, bookkeeping. */
+int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
+                      const fc_model* draft, const fc_cache* dcache,
+                      const fc_spec_state* st, void* work, int64_t work_bytes, void* stream);
+
+/* Accept/reject step alone on given logits (flaxchat/engine.py:525-592);
+ * updates the state like fc_spec_round does. */
+int32_t fc_spec_accept(const fc_spec_state* st, void* stream);
+
+/* generate_fast sampling step (flaxchat/engine.py:308-324, 343-368): for
+ * rows with !done[b] && pos[b] < max_pos[b], sample from logits row b,
+ * write it at gen[b][pos[b]+1] and tok_cur[b], advance pos and step, set
+ * done on eos. */
+int32_t fc_fast_sample(const float* logits, int32_t batch, int32_t V, float temperature,
+                       int32_t top_k, uint64_t seed, int32_t eos, int32_t* gen, int32_t gen_cap,
+                       int32_t* pos, int32_t* done, int32_t* step, const int32_t* max_pos,
+                       int32_t* tok_cur, fc_rowstat* stats, void* stream);
+
+/* Stream capture into a replayable hipGraph (the captured draft loop). */
+int32_t fc_graph_begin(void* stream);
+int32_t fc_graph_end(void* stream, void** exec_out);
+int32_t fc_graph_launch(void* exec, void* stream);
+int32_t fc_graph_destroy(void* exec);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

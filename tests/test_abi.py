@@ -1,0 +1,82 @@
+"""CPU checks of the C-ABI boundary: the library loads, exports every entry
+point include/flaxchat_amd.h declares, its structures match the ctypes
+mirror byte for byte, and argument errors come back as status codes
+(no GPU call is made)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from flaxchat_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flaxchat_amd.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(fc_\w+)\s*\(", src)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in the header but not exported"
+    assert set(_lib.EXPORTS) == set(names)
+
+
+def test_version_and_error_string():
+    L = _lib.lib()
+    assert L.fc_version() >= 100
+    assert isinstance(L.fc_last_error(), bytes)
+
+
+def test_argument_errors_are_status_codes():
+    L = _lib.lib()
+    rc = L.fc_gemm(None, None, None, 1, 1, 8, 0, 0, None)
+    assert rc == -1 and b"null" in L.fc_last_error()
+    rc = L.fc_attention(None, None, None, None, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None, 0, None)
+    assert rc == -1
+    st = _lib.FcSpecState()
+    assert L.fc_spec_accept(ctypes.byref(st), None) == -1
+
+
+def test_struct_layout_matches_c(tmp_path):
+    """Compile a C probe against the header and compare sizes and offsets."""
+    fields = {
+        "fc_layer": _lib.FcLayer, "fc_model": _lib.FcModel, "fc_cache": _lib.FcCache,
+        "fc_chunk": _lib.FcChunk, "fc_rowstat": _lib.FcRowstat, "fc_spec_state": _lib.FcSpecState,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for cname, cls in fields.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0;}")
+    c = tmp_path / "probe.c"
+    c.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", str(c), "-o", str(exe)], check=True)
+    out = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                         check=True).stdout.split("\n") if l)
+    for cname, cls in fields.items():
+        assert int(out[cname]) == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert int(out[f"{cname}.{fname}"]) == getattr(cls, fname).offset, f"{cname}.{fname}"
+
+
+def test_workspace_size_query_needs_no_gpu():
+    from flaxchat_amd.config import GPTConfig
+    m = _lib.FcModel()
+    m.n_layer, m.n_embd, m.n_head, m.n_kv_head, m.head_dim = 2, 256, 2, 2, 128
+    m.vocab = m.vocab_pad = 8192
+    m.dtype = 1
+    nb = _lib.lib().fc_forward_workspace_bytes(ctypes.byref(m), 4, 5, 5)
+    assert nb > 4 * 5 * 256 * 4 * 3
+    assert _lib.lib().fc_attention_workspace_bytes(4, 5, 6, 6, 128, 1024) > 0

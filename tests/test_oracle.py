@@ -1,0 +1,311 @@
+"""Pins the CPU restatement (oracle/) before it is trusted as the checker.
+
+Each function of the oracle is checked by something other than its own
+formula: published known-answer vectors (Philox), closed forms and
+invariants (RMSNorm, RoPE, softcap, window width), an independent float64
+full-sequence implementation of the forward written here in matrix form,
+brute force (top-k), hand-derived accept/reject cases, and the reference's
+own cross-mode test invariants (reference tests/test_engine.py:94-103,
+136-150).
+"""
+
+import numpy as np
+import pytest
+
+from flaxchat_amd.config import GPTConfig, compute_window_sizes, has_ve
+from flaxchat_amd.gpt import GPT
+from oracle import sampling as S
+from oracle.model import OracleModel, apply_rotary_emb, rms_norm, softcap
+from oracle.spec import generate_fast, generate_with_cache, spec_literal, spec_rollback
+
+
+# ---------------------------------------------------------------- Philox
+@pytest.mark.parametrize("ctr,key,expect", [
+    ((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+    ((0xffffffff,) * 4, (0xffffffff, 0xffffffff), (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+    ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+     (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1)),
+])
+def test_philox_known_answers(ctr, key, expect):
+    """Random123 philox4x32-10 known-answer vectors."""
+    got = S.philox4x32_10(np.array([ctr], np.uint64), key)[0]
+    assert tuple(int(x) for x in got) == expect
+
+
+def test_uniforms_in_range():
+    g = S.gumbel(4096, 7, 1, 2, 3)
+    assert np.all(np.isfinite(g))
+    u = S.accept_uniform(7, 0, 0, 0)
+    assert 0.0 <= u < 1.0
+
+
+# ---------------------------------------------------------------- primitives
+def test_rms_norm_unit_rms():
+    x = np.random.default_rng(0).standard_normal((5, 300)).astype(np.float32) * 7
+    y = rms_norm(x)
+    np.testing.assert_allclose(np.sqrt((y.astype(np.float64) ** 2).mean(-1)), 1.0, rtol=1e-5)
+
+
+def test_rope_rotation_and_identity():
+    from flaxchat_amd.gpt import precompute_rotary_embeddings
+    cos, sin = precompute_rotary_embeddings(64, 128)
+    x = np.random.default_rng(1).standard_normal((3, 128)).astype(np.float32)
+    np.testing.assert_array_equal(apply_rotary_emb(x, cos[0], sin[0]), x)
+    y = apply_rotary_emb(x, cos[37], sin[37])
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+    # pair (i, i + d/2) rotates by -theta_i * pos: y1 = x1 c + x2 s
+    th = 37 * 100000.0 ** (-np.arange(64) * 2 / 128)
+    np.testing.assert_allclose(y[:, :64], x[:, :64] * np.cos(th) + x[:, 64:] * np.sin(th), atol=1e-4)
+    # relative-position property: <R_p q, R_p' k> depends on p - p' only
+    q, k = x[0], x[1]
+    a = apply_rotary_emb(q, cos[10], sin[10]) @ apply_rotary_emb(k, cos[3], sin[3])
+    b = apply_rotary_emb(q, cos[20], sin[20]) @ apply_rotary_emb(k, cos[13], sin[13])
+    assert abs(a - b) < 1e-3
+
+
+def test_softcap_bounds():
+    z = np.linspace(-1000, 1000, 1001).astype(np.float32)
+    s = softcap(z)
+    assert np.all(np.abs(s) <= 15.0) and np.allclose(s, -softcap(-z))
+    np.testing.assert_allclose(softcap(np.float32([0.01]))[0], 0.01, rtol=1e-5)
+
+
+def test_window_sizes_and_ve_rules():
+    """Reference tests/test_model.py:56-72 (has_ve) and :166-170 (last layer L)."""
+    assert [has_ve(i, 4) for i in range(4)] == [False, True, False, True]
+    assert [has_ve(i, 3) for i in range(3)] == [True, False, True]
+    cfg = GPTConfig(sequence_len=2048, n_layer=6, window_pattern="SSSL")
+    w = compute_window_sizes(cfg)
+    assert w[-1] == (2048, 0) and w[0] == (512, 0) and w[3] == (2048, 0)
+    assert compute_window_sizes(cfg.with_(short_window=1024))[0] == (1024, 0)
+
+
+# ---------------------------------------------------------------- forward vs independent float64
+def _independent_forward(model, tokens):
+    """Full-sequence float64 forward in matrix form: causal + window mask
+    matrix (reference CausalSelfAttention.__call__, flaxchat/gpt.py:101-148)
+    with the decode smear recurrence x_t = n_t + g_t x_{t-1}
+    (flaxchat/engine.py:85-87). Written independently of oracle/model.py."""
+    c = model.config
+    T, D, H, G = len(tokens), c.n_embd, c.n_head, c.n_kv_head
+    d = D // H
+    f = lambda a: np.asarray(a, np.float64)
+    def rms(x):
+        return x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6)
+    sig = lambda z: 1 / (1 + np.exp(-z))
+    inv = 1.0 / (100000.0 ** (np.arange(0, d, 2) / d))
+    ang = np.arange(T)[:, None] * inv[None, :]
+    cos, sin = np.cos(ang), np.sin(ang)
+    def rope(x):  # x (T, n, d)
+        x1, x2 = x[..., :d // 2], x[..., d // 2:]
+        cc, ss = cos[:, None, :], sin[:, None, :]
+        return np.concatenate([x1 * cc + x2 * ss, -x1 * ss + x2 * cc], -1)
+    n = rms(f(model.wte.embedding)[tokens])
+    gates = f(model.smear_lambda)[0] * sig(n[:, :24] @ f(model.smear_gate.kernel))[:, 0]
+    x = np.zeros_like(n)
+    prev = np.zeros(D)
+    for t in range(T):
+        prev = n[t] + gates[t] * prev
+        x[t] = prev
+    x0 = x.copy()
+    xb = np.zeros_like(x)
+    qp, kp = np.arange(T)[:, None], np.arange(T)[None, :]
+    for i, blk in enumerate(model.blocks):
+        x = f(model.resid_lambdas)[i] * x + f(model.x0_lambdas)[i] * x0
+        h = rms(x)
+        a = blk.attn
+        q = (h @ f(a.c_q.kernel)).reshape(T, H, d)
+        k = (h @ f(a.c_k.kernel)).reshape(T, G, d)
+        v = (h @ f(a.c_v.kernel)).reshape(T, G, d)
+        if str(i) in model.value_embeds:
+            gv = 3 * sig(h[:, :12] @ f(a.ve_gate.kernel))
+            v = v + gv[..., None] * f(model.value_embeds[str(i)].embedding)[tokens].reshape(T, G, d)
+        q, k = rms(rope(q)) * 1.2, rms(rope(k)) * 1.2
+        k, v = np.repeat(k, H // G, 1), np.repeat(v, H // G, 1)
+        W = model.window_sizes[i][0]
+        mask = kp <= qp
+        if W > 0:
+            mask &= (qp - kp) <= W
+        s = np.einsum("thd,shd->hts", q, k) / np.sqrt(d)
+        s = np.where(mask[None], s, -np.inf)
+        s = np.exp(s - s.max(-1, keepdims=True))
+        s /= s.sum(-1, keepdims=True)
+        y = np.einsum("hts,shd->thd", s, v).reshape(T, D)
+        x = x + y @ f(a.c_proj.kernel)
+        x = x + np.maximum(rms(x) @ f(blk.mlp.c_fc.kernel), 0) ** 2 @ f(blk.mlp.c_proj.kernel)
+        if i == c.n_layer // 2:
+            xb = x.copy()
+    x = rms(x - f(model.backout_lambda)[0] * xb)
+    z = (x @ f(model.lm_head_kernel()))[:, :c.vocab_size]
+    return 15 * np.tanh(z / 15)
+
+
+@pytest.mark.parametrize("G,pattern,sw", [(2, "SL", 3), (1, "SSL", 5), (4, "L", None)])
+def test_forward_vs_independent_float64(G, pattern, sw):
+    cfg = GPTConfig(sequence_len=64, vocab_size=128, n_layer=3, n_head=4, n_kv_head=G, n_embd=64,
+                    window_pattern=pattern, short_window=sw)
+    m = GPT.init_normal(cfg, seed=G, std=0.15).perturb_scalars(seed=G)
+    toks = np.random.default_rng(G).integers(0, 128, 20).tolist()
+    om = OracleModel(m)
+    st = om.new_state(32)
+    got = np.stack([om.step(t, i, st) for i, t in enumerate(toks)])
+    ref = _independent_forward(m, toks)
+    assert np.abs(got - ref).max() < 2e-4
+
+
+def test_window_is_inclusive():
+    """A layer with window W sees exactly W + 1 keys (pos - j <= W): the
+    logits change when the key at distance W changes, and do not when the
+    key at distance W + 1 changes."""
+    cfg = GPTConfig(sequence_len=64, vocab_size=64, n_layer=1, n_head=2, n_kv_head=2, n_embd=64,
+                    window_pattern="S", short_window=4)
+    m = GPT.init_normal(cfg, seed=3, std=0.3)
+    m.window_sizes[0] = (4, 0)  # force a windowed single layer (the last layer is normally L)
+    om = OracleModel(m)
+    base = [1, 2, 3, 4, 5, 6, 7, 8]
+    def last(tokens):
+        st = om.new_state(16)
+        for i, t in enumerate(tokens):
+            om.step(t, i, st, need_logits=False)
+        # perturb the cached value at a chosen distance, recompute the final query
+        return st
+    st = last(base)
+    p = len(base) - 1
+    ref = om.step(base[-1], p, st)
+    for dist, changes in ((4, True), (5, False)):
+        st2 = last(base)
+        st2.v[0, p - dist] += 10.0
+        assert (np.abs(om.step(base[-1], p, st2) - ref).max() > 1e-6) == changes
+
+
+# ---------------------------------------------------------------- top-k / probs
+def test_topk_keep_brute_force():
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        V = int(rng.integers(5, 60))
+        z = np.round(rng.standard_normal(V) * 2).astype(np.float32)  # many ties
+        k = int(rng.integers(1, V))
+        keep = S.topk_keep(z, k)
+        assert keep.sum() == k
+        # every kept value >= every dropped value; among equal values lower index kept first
+        kv, dv = z[keep], z[~keep]
+        assert kv.min() >= dv.max()
+        tau = kv.min()
+        ties = np.where(z == tau)[0]
+        kept_ties = ties[keep[ties]]
+        assert np.array_equal(kept_ties, ties[:len(kept_ties)])
+
+
+def test_probs_sum_and_greedy():
+    z = np.random.default_rng(2).standard_normal(1000).astype(np.float32)
+    p = S.get_probs(z, 0.7, 40)
+    assert abs(p.sum() - 1) < 1e-5 and (p > 0).sum() == 40
+    g = S.get_probs(z, 0.0, 40)
+    assert g.sum() == 1 and int(np.argmax(g)) == int(np.argmax(z))
+
+
+# ---------------------------------------------------------------- accept KATs
+def _peaked(V, idx, hi=8.0):
+    z = np.zeros(V, np.float32)
+    z[idx] = hi
+    return z
+
+
+def test_accept_greedy_full():
+    V = 16
+    d = [3, 5, 7]
+    P = np.stack([_peaked(V, 3), _peaked(V, 5), _peaked(V, 7), _peaked(V, 9)])
+    e, a, rej, bonus = S.accept_round(P, np.zeros((3, V), np.float32), d, 0.0, None, 0, 0, 0)
+    assert e == [3, 5, 7, 9] and a == 3 and rej == -1 and bonus
+
+
+def test_accept_greedy_mid_reject():
+    V = 16
+    P = np.stack([_peaked(V, 3), _peaked(V, 6), _peaked(V, 7), _peaked(V, 9)])
+    e, a, rej, bonus = S.accept_round(P, np.zeros((3, V), np.float32), [3, 5, 7], 0.0, None, 0, 0, 0)
+    assert e == [3, 6] and a == 2 and rej == 1 and not bonus
+
+
+def test_accept_greedy_last_index_quirk():
+    """flaxchat/engine.py:541, 573: the correction counts as accepted, so a
+    rejection at the last draft still samples a bonus from the logits that
+    followed the rejected draft."""
+    V = 16
+    P = np.stack([_peaked(V, 3), _peaked(V, 5), _peaked(V, 8), _peaked(V, 9)])
+    e, a, rej, bonus = S.accept_round(P, np.zeros((3, V), np.float32), [3, 5, 7], 0.0, None, 0, 0, 0)
+    assert e == [3, 5, 8, 9] and a == 3 and rej == 2 and bonus
+
+
+def test_accept_q_zero_branch():
+    """flaxchat/engine.py:548-552: a draft token outside the draft's top-k has
+    q == 0 and is replaced by a sample from p."""
+    V = 32
+    Q = np.full((2, V), -5.0, np.float32)
+    Q[:, :4] = [4, 3, 2, 1]
+    P = np.stack([_peaked(V, 20, 30.0), _peaked(V, 1), _peaked(V, 2)])
+    e, a, rej, bonus = S.accept_round(P, Q, [31, 0], 1.0, 4, 0, 0, 0)
+    assert a == 1 and rej == 0 and e == [20] and not bonus
+    # with a single draft the same rejection is at the last index: bonus follows
+    e, a, rej, bonus = S.accept_round(P[:2], Q[:1], [31], 1.0, 4, 0, 0, 0)
+    assert a == 1 and rej == 0 and e == [20, 1] and bonus
+
+
+def test_accept_residual_and_identical_dists():
+    V = 8
+    Z = np.random.default_rng(0).standard_normal((3, V)).astype(np.float32)
+    # p == q: every ratio is 1, u < 1 always accepts
+    e, a, rej, bonus = S.accept_round(np.concatenate([Z, Z[:1]]), Z, [1, 2, 3], 1.0, None, 5, 0, 0)
+    assert a == 3 and rej == -1 and bonus and e[:3] == [1, 2, 3]
+    # p puts no mass on the draft: ratio 0 rejects, residual = p; one draft
+    # means the rejection is at the last index, so the bonus follows
+    P = np.stack([_peaked(V, 6, 40.0), _peaked(V, 4, 40.0)])
+    Q = np.stack([_peaked(V, 2, 40.0)])
+    e, a, rej, bonus = S.accept_round(P, Q, [2], 1.0, None, 5, 0, 0)
+    assert e == [6, 4] and rej == 0 and a == 1 and bonus
+
+
+# ---------------------------------------------------------------- spec state machine
+def _tiny(seed=0, L=3, G=1, Ld=1, sw=8):
+    cfg = GPTConfig(sequence_len=64, vocab_size=128, n_layer=L, n_head=2, n_kv_head=G, n_embd=64,
+                    window_pattern="SL", short_window=sw)
+    t = GPT.init_normal(cfg, seed=seed, std=0.12).perturb_scalars(seed=seed)
+    return t, t.make_draft(Ld)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("T,top_k,k", [(0.0, 40, 4), (1.0, 40, 3), (0.8, None, 5), (1.0, 3, 2)])
+def test_literal_equals_rollback(seed, T, top_k, k):
+    t, d = _tiny(seed)
+    prompt = np.random.default_rng(seed).integers(0, 128, 5 + seed).tolist()
+    a = spec_literal(t, d, prompt, max_tokens=25, temperature=T, top_k=top_k, seed=seed, draft_steps=k)
+    b = spec_rollback(t, d, prompt, max_tokens=25, temperature=T, top_k=top_k, seed=seed, draft_steps=k)
+    assert a == b and len(a) == len(prompt) + 25
+
+
+def test_spec_draft_equals_target_is_cached_greedy():
+    """Reference tests/test_engine.py:136-150."""
+    t, _ = _tiny(4)
+    prompt = [0, 1, 2, 3, 4]
+    assert spec_literal(t, t, prompt, max_tokens=8, temperature=0, draft_steps=4) == \
+        generate_with_cache(t, prompt, max_tokens=8, temperature=0)
+
+
+def test_fast_matches_cached():
+    """Reference tests/test_engine.py:94-103 (greedy) and the same stream
+    under sampling (both use draw (row, step, 0))."""
+    t, _ = _tiny(5)
+    prompt = [0, 1, 2, 3, 4]
+    for T in (0.0, 0.9):
+        a = generate_with_cache(t, prompt, max_tokens=8, temperature=T, top_k=5, seed=1)
+        b = generate_fast(t, prompt, max_tokens=8, temperature=T, top_k=5, seed=1, eos_token=-1)
+        assert a == b
+
+
+def test_fast_eos_first_token():
+    """flaxchat/engine.py:333: an EOS as the first sample ends generation
+    with the EOS kept."""
+    t, _ = _tiny(6)
+    prompt = [7, 8, 9]
+    first = generate_fast(t, prompt, max_tokens=4, temperature=0, eos_token=-1)[3]
+    out = generate_fast(t, prompt, max_tokens=4, temperature=0, eos_token=first)
+    assert out == prompt + [first]
