@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "libflaxchat_amd.so")
 FC_F32, FC_BF16 = 0, 1
 EPI_STORE, EPI_ADD, EPI_RELU2, EPI_SOFTCAP = 0, 1, 2, 4
 RES_STRIDE = 40
+PMAX = 16  # FC_PMAX: pending tokens per row and model
 
 
 class FcLayer(Structure):
@@ -85,9 +86,9 @@ def _declare(L):
     L.fc_row_stats.argtypes = [vp, i32, i32, f32, i32, vp, vp]
     L.fc_row_stats.restype = i32
     L.fc_spec_round.argtypes = [POINTER(FcModel), POINTER(FcCache), POINTER(FcModel), POINTER(FcCache),
-                                POINTER(FcSpecState), vp, i64, vp]
+                                POINTER(FcSpecState), i32, i32, vp, i64, vp]
     L.fc_spec_round.restype = i32
-    L.fc_spec_accept.argtypes = [POINTER(FcSpecState), vp]
+    L.fc_spec_accept.argtypes = [POINTER(FcSpecState), i32, vp]
     L.fc_spec_accept.restype = i32
     L.fc_fast_sample.argtypes = [vp, i32, i32, f32, i32, c_uint64, i32, vp, i32, vp, vp, vp, vp, vp, vp, vp]
     L.fc_fast_sample.restype = i32

@@ -66,28 +66,94 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
   }
 }
 
-// h = x * rsqrt(mean(x^2) + 1e-6) (flaxchat/gpt.py:44-46). With n_out > 0,
-// output row m reads input row (m / n_out) * W + (W - n_out) + m % n_out
-// (the head only needs the last n_out slots of each row).
+// A residual-stream update left pending by a split-K GEMM: the S partial
+// products in part[S][rows][D] still have to be added to x, with the
+// epilogue of that GEMM (EPI_ADD: x += y; EPI_MLPOUT: residual add, backout
+// capture, then the next layer's lambda mix or the final backout).
+struct Pending {
+  int S, mode, rows;
+  const float* part;
+  const float* x0;
+  float* xb;
+  float r, a, lb;
+  int capture, last;
+};
+
+// h = x * rsqrt(mean(x^2) + 1e-6) (flaxchat/gpt.py:44-46), after applying a
+// pending update to x. With n_out > 0, output row m reads input row
+// (m / n_out) * W + (W - n_out) + m % n_out (the head only needs the last
+// n_out slots of each row).
+#define NORM_MAXV 4  // float4 per thread: D <= 4096
 template <typename TO>
-__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, TO* __restrict__ h, int D, int W,
-                                                 int n_out) {
+__global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __restrict__ h, int D, int W, int n_out,
+                                                 Pending p) {
   __shared__ float red[16];
-  const int row = blockIdx.x;
+  const int row = blockIdx.x, tid = threadIdx.x;
   const int64_t in_row = n_out > 0 ? (int64_t)(row / n_out) * W + (W - n_out) + row % n_out : row;
-  const float* xr = x + in_row * D;
+  const int D4 = D >> 2;
+  float4* xr = (float4*)(x + in_row * D);
+  float4 v[NORM_MAXV];
   float ss = 0.f;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) ss += xr[d] * xr[d];
+#pragma unroll
+  for (int u = 0; u < NORM_MAXV; ++u) {
+    const int i = tid + 256 * u;
+    if (i < D4) {
+      float4 t = xr[i];
+      if (p.S > 0) {
+        // all split partials of this float4 are loaded together, summed in order
+        float4 pp[FC_MAX_SPLIT];
+#pragma unroll
+        for (int s = 0; s < FC_MAX_SPLIT; ++s)
+          if (s < p.S) pp[s] = ((const float4*)(p.part + ((int64_t)s * p.rows + in_row) * D))[i];
+#pragma unroll
+        for (int s = 0; s < FC_MAX_SPLIT; ++s)
+          if (s < p.S) {
+            t.x += pp[s].x; t.y += pp[s].y; t.z += pp[s].z; t.w += pp[s].w;
+          }
+        if (p.mode == EPI_MLPOUT) {
+          const int64_t o = in_row * D4 + i;
+          float4 xb_v = {0.f, 0.f, 0.f, 0.f};
+          if (p.capture) {
+            ((float4*)p.xb)[o] = t;
+            xb_v = t;
+          } else if (p.last) {
+            xb_v = ((const float4*)p.xb)[o];
+          }
+          if (p.last) {
+            t.x = t.x - p.lb * xb_v.x; t.y = t.y - p.lb * xb_v.y;
+            t.z = t.z - p.lb * xb_v.z; t.w = t.w - p.lb * xb_v.w;
+          } else {
+            const float4 z = ((const float4*)p.x0)[o];
+            t.x = p.r * t.x + p.a * z.x; t.y = p.r * t.y + p.a * z.y;
+            t.z = p.r * t.z + p.a * z.z; t.w = p.r * t.w + p.a * z.w;
+          }
+        }
+        xr[i] = t;
+      }
+      v[u] = t;
+      ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+    }
+  }
   ss = block_sum(ss, red);
   const float inv = 1.f / sqrtf(ss / (float)D + 1e-6f);
   TO* hr = h + (int64_t)row * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) st<TO>(hr, d, xr[d] * inv);
+#pragma unroll
+  for (int u = 0; u < NORM_MAXV; ++u) {
+    const int i = tid + 256 * u;
+    if (i < D4) {
+      st<TO>(hr, 4 * i + 0, v[u].x * inv);
+      st<TO>(hr, 4 * i + 1, v[u].y * inv);
+      st<TO>(hr, 4 * i + 2, v[u].z * inv);
+      st<TO>(hr, 4 * i + 3, v[u].w * inv);
+    }
+  }
 }
 
 struct FwdWork {
   float *x, *x0, *xb, *qkv;
   void *h, *q, *y, *hid, *part;
   int64_t part_bytes, total;
+  GemmWork gw;
 };
 
 static FwdWork carve(const fc_model* m, int B, int W, int max_keys, char* base) {
@@ -111,6 +177,10 @@ static FwdWork carve(const fc_model* m, int B, int W, int max_keys, char* base) 
   w.hid = take(M * 4 * D * es);
   w.part_bytes = fc_attn_part_bytes(B, W, H, G, hd, max_keys);
   w.part = take(w.part_bytes);
+  // split-K partials of the two GEMMs that write the residual stream
+  int64_t gp = std::max(fc_gemm_part_bytes((int)M, D, H * hd), fc_gemm_part_bytes((int)M, D, 4 * D));
+  w.gw.part = (float*)take(gp);
+  w.gw.part_bytes = gp;
   w.total = off;
   return w;
 }
@@ -127,7 +197,8 @@ static int check_model(const fc_model* m) {
   FC_CHECK_ARG(m->dtype == FC_F32 || m->dtype == FC_BF16, "dtype");
   FC_CHECK_ARG(m->n_head > 0 && m->n_kv_head > 0 && m->n_head % m->n_kv_head == 0, "heads");
   FC_CHECK_ARG(m->head_dim * m->n_head == m->n_embd, "head_dim * n_head must equal n_embd");
-  FC_CHECK_ARG(m->n_embd % 8 == 0 && m->n_embd >= 24, "n_embd must be a multiple of 8 and >= 24");
+  FC_CHECK_ARG(m->n_embd % 8 == 0 && m->n_embd >= 24 && m->n_embd <= 4096,
+               "n_embd must be a multiple of 8 in [24, 4096]");
   FC_CHECK_ARG(m->vocab > 0 && m->vocab <= m->vocab_pad, "vocab");
   return FC_OK;
 }
@@ -160,11 +231,13 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
                        ch->nvalid, W, D, c->cap, c->hist, w.x, w.x0);
   FC_LAUNCH_CHECK();
 
+  Pending pend{};
   auto norm = [&](int rows, int n_out) {
     if (dt == FC_BF16)
-      hipLaunchKernelGGL(k_rmsnorm<bf16_t>, dim3(rows), dim3(256), 0, s, w.x, (bf16_t*)w.h, D, W, n_out);
+      hipLaunchKernelGGL(k_rmsnorm<bf16_t>, dim3(rows), dim3(256), 0, s, w.x, (bf16_t*)w.h, D, W, n_out, pend);
     else
-      hipLaunchKernelGGL(k_rmsnorm<float>, dim3(rows), dim3(256), 0, s, w.x, (float*)w.h, D, W, n_out);
+      hipLaunchKernelGGL(k_rmsnorm<float>, dim3(rows), dim3(256), 0, s, w.x, (float*)w.h, D, W, n_out, pend);
+    pend = Pending{};
   };
   const int backout = m->n_layer / 2;
   for (int l = 0; l < m->n_layer; ++l) {
@@ -175,7 +248,7 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.mode = EPI_STORE;
     e.out = w.qkv;
     e.ldo = NQKV;
-    rc = fc_launch_gemm(w.h, L.wqkv, M, NQKV, D, dt, e, s);
+    rc = fc_launch_gemm(w.h, L.wqkv, M, NQKV, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
     rc = fc_launch_prologue(w.qkv, w.h, ch->tokens, m, l, c, ch->start, ch->nvalid, B, W, w.q, s);
     if (rc) return rc;
@@ -189,8 +262,15 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.mode = EPI_ADD;
     e.out = w.x;
     e.ldo = D;
-    rc = fc_launch_gemm(w.y, L.wo, M, D, H * hd, dt, e, s);
+    int S = 1;
+    rc = fc_launch_gemm(w.y, L.wo, M, D, H * hd, dt, e, w.gw, s, &S);
     if (rc) return rc;
+    if (S > 1) {
+      pend.S = S;
+      pend.mode = EPI_ADD;
+      pend.rows = M;
+      pend.part = w.gw.part;
+    }
     norm(M, 0);
     FC_LAUNCH_CHECK();
     e = Epi{};
@@ -198,7 +278,7 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.out = w.hid;
     e.ldo = 4 * D;
     e.out_dtype = dt;
-    rc = fc_launch_gemm(w.h, L.wfc, M, 4 * D, D, dt, e, s);
+    rc = fc_launch_gemm(w.h, L.wfc, M, 4 * D, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
     e = Epi{};
     e.mode = EPI_MLPOUT;
@@ -213,8 +293,22 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
       e.r = m->layers[l + 1].resid_lambda;
       e.a = m->layers[l + 1].x0_lambda;
     }
-    rc = fc_launch_gemm(w.hid, L.wproj, M, D, 4 * D, dt, e, s);
+    S = 1;
+    rc = fc_launch_gemm(w.hid, L.wproj, M, D, 4 * D, dt, e, w.gw, s, &S);
     if (rc) return rc;
+    if (S > 1) {
+      pend.S = S;
+      pend.mode = EPI_MLPOUT;
+      pend.rows = M;
+      pend.part = w.gw.part;
+      pend.x0 = w.x0;
+      pend.xb = w.xb;
+      pend.r = e.r;
+      pend.a = e.a;
+      pend.lb = e.lb;
+      pend.capture = e.capture;
+      pend.last = e.last;
+    }
   }
   if (ch->n_out > 0) {
     const int Mo = B * ch->n_out;
@@ -226,7 +320,7 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.n_out = ch->n_out;
     e.row_stride = ch->logits_stride;
     e.V = m->vocab;
-    rc = fc_launch_gemm(w.h, m->lm_head, Mo, m->vocab_pad, D, dt, e, s);
+    rc = fc_launch_gemm(w.h, m->lm_head, Mo, m->vocab_pad, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
   }
   return FC_OK;

@@ -7,53 +7,61 @@
 // layer (engine.py:94), the backout capture and subtraction
 // (engine.py:164-166) and the 15*tanh(z/15) softcap (engine.py:173-174).
 //
-// Three kernels, chosen by M (= rows = batch x tokens per row):
-//   k_gemv      VALU dot products; fp32 weights (parity mode) or bf16 with
-//               M < 16, where a 16-row matrix-core tile would be mostly empty.
-//   k_gemm_sk   bf16 MFMA 16x16x32, 16 output columns per workgroup, the
-//               four waves split K and reduce through LDS (M <= 64).
-//   k_gemm_wide bf16 MFMA, 64 columns per workgroup, the A tile staged in
-//               LDS and shared by the four waves (M > 64).
-// Weights stream from HBM exactly once per M tile; each lane loads 16 bytes
-// per row segment so a wave reads 64 contiguous bytes of each of 16 rows.
+// Kernels, chosen by M (= rows = batch x tokens per row):
+//   k_gemv        VALU dot products; fp32 weights (parity mode) or bf16 with
+//                 M < 16, where a 16-row matrix-core tile would be mostly empty.
+//   k_gemm_stream bf16 MFMA 16x16x32 for M <= 64 (draft steps): pure weight
+//                 streaming. A workgroup owns 16 output columns; its four
+//                 waves split K and each wave issues the 16-byte weight loads
+//                 of up to four 128-wide k chunks before the first MFMA, so
+//                 ~16 KB per wave are in flight; the activation rows come
+//                 straight from L2.
+//   k_gemm_tile   bf16 MFMA for M > 64 (verify / prefill). A workgroup owns
+//                 up to 256 rows x 128 columns; the activation chunk is staged
+//                 in LDS (double buffered) and each wave reuses every A
+//                 fragment for two 16-column blocks, halving LDS traffic per
+//                 MFMA; weight fragments for the next chunk are prefetched.
+// When N alone gives too few workgroups to occupy 256 CUs, a GEMM whose
+// output is the fp32 residual stream may split K across workgroups: each
+// split writes its partial product with plain stores and the RMSNorm kernel
+// that consumes x next sums the splits in fixed order and applies the
+// epilogue (a kernel boundary is the only synchronisation; on MI355X the
+// eight XCD L2 caches are not coherent, so an in-kernel device-scope fence
+// would write back a whole L2 per workgroup).
 #include "fc_common.h"
 #include "fc_internal.h"
 
-__device__ __forceinline__ void epi_apply(const Epi& e, int m, int n, float acc) {
-  switch (e.mode) {
-    case EPI_STORE: {
-      ((float*)e.out)[(int64_t)m * e.ldo + n] = acc;
-      break;
+template <int EPI>
+__device__ __forceinline__ void epi_apply(const Epi e, int m, int n, float acc) {
+  if constexpr (EPI == EPI_STORE) {
+    ((float*)e.out)[(int64_t)m * e.ldo + n] = acc;
+  } else if constexpr (EPI == EPI_ADD) {
+    float* o = (float*)e.out + (int64_t)m * e.ldo + n;
+    *o = *o + acc;
+  } else if constexpr (EPI == EPI_RELU2) {
+    float r = fmaxf(acc, 0.f);
+    r = r * r;
+    if (e.out_dtype == FC_BF16) ((bf16_t*)e.out)[(int64_t)m * e.ldo + n] = f2bf(r);
+    else ((float*)e.out)[(int64_t)m * e.ldo + n] = r;
+  } else if constexpr (EPI == EPI_MLPOUT) {
+    const int64_t i = (int64_t)m * e.ldo + n;
+    float* x = (float*)e.out;
+    const float t = x[i] + acc;  // x + mlp(...)                 engine.py:161
+    float xb_v = 0.f;
+    if (e.capture) {             // x_backout                    engine.py:164
+      e.xb[i] = t;
+      xb_v = t;
+    } else if (e.last) {
+      xb_v = e.xb[i];
     }
-    case EPI_ADD: {
-      float* o = (float*)e.out + (int64_t)m * e.ldo + n;
-      *o = *o + acc;
-      break;
-    }
-    case EPI_RELU2: {
-      float r = fmaxf(acc, 0.f);
-      r = r * r;
-      if (e.out_dtype == FC_BF16) ((bf16_t*)e.out)[(int64_t)m * e.ldo + n] = f2bf(r);
-      else ((float*)e.out)[(int64_t)m * e.ldo + n] = r;
-      break;
-    }
-    case EPI_MLPOUT: {
-      const int64_t i = (int64_t)m * e.ldo + n;
-      float* x = (float*)e.out;
-      const float t = x[i] + acc;             // x + mlp(...)        engine.py:161
-      float xb_v = 0.f;
-      if (e.capture) { e.xb[i] = t; xb_v = t; } // x_backout          engine.py:164
-      else if (e.last) xb_v = e.xb[i];
-      if (e.last) x[i] = t - e.lb * xb_v;       // x - lambda * x_b    engine.py:166
-      else x[i] = e.r * t + e.a * e.x0[i];      // next layer's mix    engine.py:94
-      break;
-    }
-    case EPI_SOFTCAP: {
-      if (n < e.V) {
-        const int b = m / e.n_out, rr = m - b * e.n_out;
-        ((float*)e.out)[(int64_t)b * e.row_stride + (int64_t)rr * e.V + n] = 15.f * tanhf(acc / 15.f);
-      }
-      break;
+    if (e.last) x[i] = t - e.lb * xb_v;      // x - lambda * x_b  engine.py:166
+    else x[i] = e.r * t + e.a * e.x0[i];     // next layer's mix  engine.py:94
+  } else if constexpr (EPI == EPI_PARTIAL) {  // split-K partial, finished by the next RMSNorm
+    e.part[((int64_t)e.split * e.part_rows + m) * e.ldo + n] = acc;
+  } else {                                   // EPI_SOFTCAP
+    if (n < e.V) {
+      const int b = m / e.n_out, rr = m - b * e.n_out;
+      ((float*)e.out)[(int64_t)b * e.row_stride + (int64_t)rr * e.V + n] = 15.f * tanhf(acc / 15.f);
     }
   }
 }
@@ -70,11 +78,6 @@ __device__ __forceinline__ void load_vec<float, 4>(const float* p, float* o) {
   o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
 }
 template <>
-__device__ __forceinline__ void load_vec<float, 8>(const float* p, float* o) {
-  load_vec<float, 4>(p, o);
-  load_vec<float, 4>(p + 4, o + 4);
-}
-template <>
 __device__ __forceinline__ void load_vec<bf16_t, 8>(const bf16_t* p, float* o) {
   uint4 v = *(const uint4*)p;
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -84,18 +87,10 @@ __device__ __forceinline__ void load_vec<bf16_t, 8>(const bf16_t* p, float* o) {
     o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
   }
 }
-template <>
-__device__ __forceinline__ void load_vec<bf16_t, 4>(const bf16_t* p, float* o) {
-  uint2 v = *(const uint2*)p;
-  o[0] = __uint_as_float(v.x << 16);
-  o[1] = __uint_as_float(v.x & 0xffff0000u);
-  o[2] = __uint_as_float(v.y << 16);
-  o[3] = __uint_as_float(v.y & 0xffff0000u);
-}
 
-template <typename T, int MB>
-__global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* __restrict__ W,
-                                              int M, int N, int K, Epi e) {
+template <typename T, int MB, int EPI>
+__global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* __restrict__ W, int M, int N,
+                                              int K, Epi e) {
   constexpr int VEC = 16 / sizeof(T);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * 4;
@@ -130,160 +125,308 @@ __global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* 
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[i][c] = wave_sum(acc[i][c]);
-  // spread the stores over lanes: lane (i*4 + c) stores element (i, c)
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      if (lane == ((i * 4 + c) & 63) && m0 + i < M && n0 + c < N) epi_apply(e, m0 + i, n0 + c, acc[i][c]);
+      if (lane == ((i * 4 + c) & 63) && m0 + i < M && n0 + c < N) epi_apply<EPI>(e, m0 + i, n0 + c, acc[i][c]);
 }
 
 // ---------------------------------------------------------------------------
 // bf16 MFMA 16x16x32. Operand layout (wave64): lane l holds row (l % 16) of
-// A / column (l % 16) of B and the 8 consecutive k values 8*(l/16)..+7 of a
+// A / column (l % 16) of B and 8 consecutive k values 8*(l/16)..+7 of a
 // 32-wide k step; the f32x4 result holds rows 4*(l/16)+i of column l % 16.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(v4u a, v4u b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
 }
 
-template <int MB>
-__global__ __launch_bounds__(256) void k_gemm_sk(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
-                                                 int M, int N, int K, Epi e) {
+// M <= 64: streaming. grid (N/64, S, ceil(M/(16 MB))). A workgroup owns 64
+// columns (4 N-blocks) so each activation fragment fetched from L2 feeds four
+// MFMAs; its four waves split K in 128-wide chunks and each wave keeps two
+// chunks of weight fragments (32 KB per wave) in flight.
+template <int MB, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_stream(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                     int M, int N, int K, int S, Epi e) {
+  constexpr int NB = 4, U = 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int m0 = blockIdx.y * 16 * MB;
-  f32x4 acc[MB];
+  const int n0 = blockIdx.x * 64;
+  const int s = blockIdx.y;
+  const int m0 = blockIdx.z * 16 * MB;
+  const int C = K >> 7;
+  const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
+  f32x4 acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16_t* wrow = W + (int64_t)(n0 + r) * K + 8 * g;
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  for (int kc = wave * 128; kc < K; kc += 512) {
-    uint4 wf[4];
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) wf[s] = *(const uint4*)(wrow + kc + 32 * s);
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bf16_t* wbase = W + (int64_t)(n0 + r) * K + 8 * g;
+  const bf16_t* abase[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int am = m0 + 16 * mb + r;
-      const bf16_t* arow = A + (int64_t)am * K + kc + 8 * g;
+  for (int mb = 0; mb < MB; ++mb) abase[mb] = A + (int64_t)min(m0 + 16 * mb + r, M - 1) * K + 8 * g;
+  for (int c0 = c_beg + wave; c0 < c_end; c0 += 4 * U) {
+    v4u wf[U][NB][4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint4 af = am < M ? *(const uint4*)(arow + 32 * s) : zero;
-        acc[mb] = mfma16(af, wf[s], acc[mb]);
+    for (int u = 0; u < U; ++u) {
+      const int c = min(c0 + 4 * u, c_end - 1);  // a clamped duplicate chunk is loaded, never used
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wf[u][j][st] = *(const v4u*)(wbase + (int64_t)16 * j * K + c * 128 + 32 * st);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 4 * u;
+      if (c < c_end) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          v4u af[4];
+#pragma unroll
+          for (int st = 0; st < 4; ++st) af[st] = *(const v4u*)(abase[mb] + c * 128 + 32 * st);
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[mb][j] = mfma16(af[st], wf[u][j][st], acc[mb][j]);
+        }
       }
     }
   }
-  __shared__ f32x4 red[3][MB][64];
+  __shared__ f32x4 red[3][MB * NB][64];
   if (wave > 0)
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) red[wave - 1][mb * NB + j][lane] = acc[mb][j];
   __syncthreads();
   if (wave == 0) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      f32x4 t = acc[mb];
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int w = 0; w < 3; ++w) t += red[w][mb][lane];
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 16 * mb + 4 * g + i;
-        if (m < M) epi_apply(e, m, n0 + r, t[i]);
-      }
-    }
+        for (int w = 0; w < 3; ++w) acc[mb][j] += red[w][mb * NB + j][lane];
+  }
+  Epi ee = e;
+  ee.split = s;
+  if (wave == 0) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + 16 * mb + 4 * g + i;
+          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * j + r, acc[mb][j][i]);
+        }
   }
 }
 
-template <int MB>
-__global__ __launch_bounds__(256) void k_gemm_wide(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
-                                                   int M, int N, int K, Epi e) {
-  constexpr int LDA = 128 + 8;  // bf16 elements per LDS row (padded)
-  __shared__ bf16_t As[16 * MB * LDA];
+// M > 64: LDS-staged activations. grid (N/128, S, ceil(M/(16 MB))).
+template <int MB, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_tile(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                   int M, int N, int K, int S, Epi e) {
+  constexpr int NB = 2, KC = 64, LDA = KC + 8, ROWS = 16 * MB;
+  constexpr int PASSES = ROWS / 32;  // 32 rows x 64 k per 256-thread pass
+  static_assert(ROWS % 32 == 0, "tile rows must be a multiple of 32");
+  __shared__ bf16_t As[2][ROWS * LDA];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 64 + wave * 16;
-  const int m0 = blockIdx.y * 16 * MB;
-  f32x4 acc[MB];
+  const int nw = blockIdx.x * 128 + wave * 32;
+  const int s = blockIdx.y;
+  const int m0 = blockIdx.z * ROWS;
+  const int C = K / KC;
+  const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
+  f32x4 acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16_t* wrow = W + (int64_t)(n0 + r) * K + 8 * g;
-  const int srow = t >> 4, scol = (t & 15) * 8;
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint4 zero = {0u, 0u, 0u, 0u};
-  for (int kc = 0; kc < K; kc += 128) {
-    uint4 wf[4];
+  const int srow = t >> 3, scol = (t & 7) * 8;
+  const bf16_t* w0 = W + (int64_t)(nw + r) * K + 8 * g;
+  const bf16_t* w1 = w0 + (int64_t)16 * K;
+
+  v4u ast[PASSES];
+  v4u wc0[2], wc1[2], wn0[2], wn1[2];
+  // prologue: chunk c_beg (every split owns >= 1 chunk)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) wf[s] = *(const uint4*)(wrow + kc + 32 * s);
-    uint4 stage[MB];
+  for (int p = 0; p < PASSES; ++p)
+    ast[p] = *(const v4u*)(A + (int64_t)min(m0 + srow + 32 * p, M - 1) * K + c_beg * KC + scol);
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const int gm = m0 + srow + 16 * i;
-      stage[i] = gm < M ? *(const uint4*)(A + (int64_t)gm * K + kc + scol) : zero;
+  for (int ks = 0; ks < 2; ++ks) {
+    wc0[ks] = *(const v4u*)(w0 + c_beg * KC + 32 * ks);
+    wc1[ks] = *(const v4u*)(w1 + c_beg * KC + 32 * ks);
+  }
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) *(v4u*)(&As[0][(srow + 32 * p) * LDA + scol]) = ast[p];
+  for (int c = c_beg; c < c_end; ++c) {
+    const int buf = (c - c_beg) & 1;
+    // prefetch the next chunk unconditionally (the last iteration re-reads its
+    // own chunk) so the staging registers never live across a branch; rows
+    // past M are clamped: computed, never stored
+    const int cn = min(c + 1, c_end - 1);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      ast[p] = *(const v4u*)(A + (int64_t)min(m0 + srow + 32 * p, M - 1) * K + cn * KC + scol);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      wn0[ks] = *(const v4u*)(w0 + cn * KC + 32 * ks);
+      wn1[ks] = *(const v4u*)(w1 + cn * KC + 32 * ks);
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < MB; ++i) *(uint4*)(As + (srow + 16 * i) * LDA + scol) = stage[i];
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const uint4 af = *(const uint4*)(As + (16 * mb + r) * LDA + 32 * s + 8 * g);
-        acc[mb] = mfma16(af, wf[s], acc[mb]);
+        const v4u af = *(const v4u*)(&As[buf][(16 * mb + r) * LDA + 32 * ks + 8 * g]);
+        acc[mb][0] = mfma16(af, wc0[ks], acc[mb][0]);
+        acc[mb][1] = mfma16(af, wc1[ks], acc[mb][1]);
       }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) *(v4u*)(&As[buf ^ 1][(srow + 32 * p) * LDA + scol]) = ast[p];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      wc0[ks] = wn0[ks];
+      wc1[ks] = wn1[ks];
+    }
   }
+  Epi ee = e;
+  ee.split = s;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + 16 * mb + 4 * g + i;
-      if (m < M) epi_apply(e, m, n0 + r, acc[mb][i]);
-    }
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mb + 4 * g + i;
+        if (m < M) epi_apply<EPI>(ee, m, nw + 16 * j + r, acc[mb][j][i]);
+      }
 }
 
 // ---------------------------------------------------------------------------
 // Dispatch
 // ---------------------------------------------------------------------------
+#define FC_EPI_SWITCH(mode, CALL)                              \
+  switch (mode) {                                              \
+    case EPI_STORE: { constexpr int E = EPI_STORE; CALL; break; }     \
+    case EPI_ADD: { constexpr int E = EPI_ADD; CALL; break; }         \
+    case EPI_RELU2: { constexpr int E = EPI_RELU2; CALL; break; }     \
+    case EPI_MLPOUT: { constexpr int E = EPI_MLPOUT; CALL; break; }   \
+    case EPI_PARTIAL: { constexpr int E = EPI_PARTIAL; CALL; break; } \
+    default: { constexpr int E = EPI_SOFTCAP; CALL; break; }          \
+  }
+
+template <typename T, int MB>
+static void launch_gemv_mb(const void* A, const void* W, int M, int N, int K, const Epi& e, hipStream_t s) {
+  const dim3 grid((N + 15) / 16, (M + MB - 1) / MB);
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemv<T, MB, E>), grid, dim3(256), 0, s, (const T*)A, (const T*)W, M,
+                                           N, K, e));
+}
 template <typename T>
 static void launch_gemv(const void* A, const void* W, int M, int N, int K, const Epi& e, hipStream_t s) {
-  dim3 blk(256);
-  if (M <= 1) {
-    hipLaunchKernelGGL((k_gemv<T, 1>), dim3((N + 15) / 16, M), blk, 0, s, (const T*)A, (const T*)W, M, N, K, e);
-  } else if (M <= 2) {
-    hipLaunchKernelGGL((k_gemv<T, 2>), dim3((N + 15) / 16, 1), blk, 0, s, (const T*)A, (const T*)W, M, N, K, e);
-  } else if (M <= 4) {
-    hipLaunchKernelGGL((k_gemv<T, 4>), dim3((N + 15) / 16, 1), blk, 0, s, (const T*)A, (const T*)W, M, N, K, e);
-  } else {
-    hipLaunchKernelGGL((k_gemv<T, 8>), dim3((N + 15) / 16, (M + 7) / 8), blk, 0, s, (const T*)A, (const T*)W, M, N,
-                       K, e);
-  }
+  if (M <= 1) launch_gemv_mb<T, 1>(A, W, M, N, K, e, s);
+  else if (M <= 2) launch_gemv_mb<T, 2>(A, W, M, N, K, e, s);
+  else if (M <= 4) launch_gemv_mb<T, 4>(A, W, M, N, K, e, s);
+  else launch_gemv_mb<T, 8>(A, W, M, N, K, e, s);
 }
 
-int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, hipStream_t s) {
+template <int MB>
+static void launch_stream(const void* A, const void* W, int M, int N, int K, int S, const Epi& e, hipStream_t s) {
+  const dim3 grid(N / 64, S, (M + 16 * MB - 1) / (16 * MB));
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_stream<MB, E>), grid, dim3(256), 0, s, (const bf16_t*)A,
+                                           (const bf16_t*)W, M, N, K, S, e));
+}
+template <int MB>
+static void launch_tile(const void* A, const void* W, int M, int N, int K, int S, const Epi& e, hipStream_t s) {
+  const dim3 grid(N / 128, S, (M + 16 * MB - 1) / (16 * MB));
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_tile<MB, E>), grid, dim3(256), 0, s, (const bf16_t*)A,
+                                           (const bf16_t*)W, M, N, K, S, e));
+}
+
+// split count so that (workgroups x S) reaches ~2 per CU, keeping >= min_chunks
+// chunks per split
+// split count so that (workgroups x S) reaches ~2 per CU, keeping >= 1 chunk
+// per split
+static int pick_split(int wgs, int chunks) {
+  if (wgs <= 0 || chunks <= 0) return 1;
+  int S = (256 + wgs - 1) / wgs;
+  return std::max(1, std::min(std::min(S, chunks), FC_MAX_SPLIT));
+}
+
+// One plan drives the workspace sizing and the launch.
+enum { GK_GEMV = 0, GK_STREAM = 1, GK_TILE = 2 };
+struct GemmPlan {
+  int kind, mb, mtiles, ntiles, S;
+};
+static GemmPlan plan_gemm(int M, int N, int K, int dtype, bool can_split) {
+  GemmPlan p{};
+  p.S = 1;
+  if (dtype == FC_F32 || M < 16 || K % 128 != 0 || N % 64 != 0) {
+    p.kind = GK_GEMV;
+    return p;
+  }
+  if (M <= 64 || N % 128 != 0) {
+    p.kind = GK_STREAM;
+    p.mb = std::min(4, (M + 15) / 16);
+    p.mtiles = (M + 16 * p.mb - 1) / (16 * p.mb);
+    p.ntiles = N / 64;
+    if (can_split) p.S = pick_split(p.ntiles * p.mtiles, K / 128);
+  } else {
+    p.kind = GK_TILE;
+    p.ntiles = N / 128;
+    // wide N: one M tile streams the weights exactly once; narrower N: 64-row
+    // M tiles multiply the workgroups (weight re-reads hit L2 / MALL)
+    if (p.ntiles >= 128) p.mb = M <= 128 ? 8 : (M <= 192 ? 12 : (M <= 224 ? 14 : 16));
+    else p.mb = 4;
+    p.mtiles = (M + 16 * p.mb - 1) / (16 * p.mb);
+    if (can_split) p.S = pick_split(p.ntiles * p.mtiles, K / 64);
+  }
+  return p;
+}
+
+int64_t fc_gemm_part_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  GemmPlan p = plan_gemm(M, N, K, FC_BF16, true);
+  return p.S > 1 ? fc_align((int64_t)p.S * M * N * 4) : 0;
+}
+
+int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, const GemmWork& gw,
+                   hipStream_t s, int* splits) {
+  if (splits) *splits = 1;
   if (M <= 0 || N <= 0) return FC_OK;
   FC_CHECK_ARG(K > 0 && K % 8 == 0, "gemm K must be a positive multiple of 8");
-  if (dtype == FC_F32) {
-    launch_gemv<float>(A, W, M, N, K, e, s);
-  } else if (M < 16 || K % 128 != 0 || N % 16 != 0) {
-    launch_gemv<bf16_t>(A, W, M, N, K, e, s);
-  } else if (M <= 64 || N % 64 != 0) {
-    const int mb = (M + 15) / 16;
-    if (mb <= 1)
-      hipLaunchKernelGGL((k_gemm_sk<1>), dim3(N / 16, 1), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W, M, N,
-                         K, e);
-    else if (mb <= 2)
-      hipLaunchKernelGGL((k_gemm_sk<2>), dim3(N / 16, 1), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W, M, N,
-                         K, e);
-    else
-      hipLaunchKernelGGL((k_gemm_sk<4>), dim3(N / 16, (M + 63) / 64), dim3(256), 0, s, (const bf16_t*)A,
-                         (const bf16_t*)W, M, N, K, e);
+  const bool can_split = splits != nullptr && gw.part != nullptr;
+  GemmPlan p = plan_gemm(M, N, K, dtype, can_split);
+  if (p.S > 1 && (int64_t)p.S * M * N * 4 > gw.part_bytes) p.S = 1;
+  Epi ee = e;
+  if (p.S > 1) {
+    ee.mode = EPI_PARTIAL;
+    ee.part = gw.part;
+    ee.part_rows = M;
+    ee.ldo = N;
+    *splits = p.S;
+  }
+  if (p.kind == GK_GEMV) {
+    if (dtype == FC_F32) launch_gemv<float>(A, W, M, N, K, ee, s);
+    else launch_gemv<bf16_t>(A, W, M, N, K, ee, s);
+  } else if (p.kind == GK_STREAM) {
+    if (p.mb == 1) launch_stream<1>(A, W, M, N, K, p.S, ee, s);
+    else if (p.mb == 2) launch_stream<2>(A, W, M, N, K, p.S, ee, s);
+    else if (p.mb == 3) launch_stream<3>(A, W, M, N, K, p.S, ee, s);
+    else launch_stream<4>(A, W, M, N, K, p.S, ee, s);
   } else {
-    if (M <= 128)
-      hipLaunchKernelGGL((k_gemm_wide<8>), dim3(N / 64, 1), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W, M,
-                         N, K, e);
-    else
-      hipLaunchKernelGGL((k_gemm_wide<16>), dim3(N / 64, (M + 255) / 256), dim3(256), 0, s, (const bf16_t*)A,
-                         (const bf16_t*)W, M, N, K, e);
+    if (p.mb == 4) launch_tile<4>(A, W, M, N, K, p.S, ee, s);
+    else if (p.mb == 8) launch_tile<8>(A, W, M, N, K, p.S, ee, s);
+    else if (p.mb == 12) launch_tile<12>(A, W, M, N, K, p.S, ee, s);
+    else if (p.mb == 14) launch_tile<14>(A, W, M, N, K, p.S, ee, s);
+    else launch_tile<16>(A, W, M, N, K, p.S, ee, s);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
@@ -302,5 +445,5 @@ extern "C" int32_t fc_gemm(const void* A, const void* W, void* out, int32_t M, i
   e.n_out = 1;
   e.row_stride = N;
   e.V = N;
-  return fc_launch_gemm(A, W, M, N, K, dtype, e, (hipStream_t)stream);
+  return fc_launch_gemm(A, W, M, N, K, dtype, e, GemmWork{}, (hipStream_t)stream, nullptr);
 }

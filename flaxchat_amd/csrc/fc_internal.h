@@ -1,8 +1,9 @@
 // Internal (not exported) declarations shared by the .hip translation units.
 #pragma once
 #include "fc_common.h"
+#include <algorithm>
 
-enum { EPI_STORE = 0, EPI_ADD = 1, EPI_RELU2 = 2, EPI_MLPOUT = 3, EPI_SOFTCAP = 4 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_RELU2 = 2, EPI_MLPOUT = 3, EPI_SOFTCAP = 4, EPI_PARTIAL = 5 };
 
 struct Epi {
   int mode;
@@ -18,9 +19,22 @@ struct Epi {
   int n_out;
   int64_t row_stride;
   int V;
+  // EPI_PARTIAL: split `split` writes part[(split * part_rows + m) * ldo + n]
+  float* part;
+  int part_rows, split;
 };
 
-int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, hipStream_t s);
+#define FC_MAX_SPLIT 8
+// split-K partials of GEMMs writing the residual stream (finished by RMSNorm)
+struct GemmWork {
+  float* part;
+  int64_t part_bytes;
+};
+int64_t fc_gemm_part_bytes(int M, int N, int K);
+// `splits` (may be NULL: no split) receives the split count; when > 1 the
+// output was written as partials to gw.part and the caller must finish it.
+int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, const GemmWork& gw,
+                   hipStream_t s, int* splits);
 
 struct AttnGrid {
   int nqblk, nsplit, split_keys;

@@ -266,25 +266,37 @@ static SpecDev to_dev(const fc_spec_state* s) {
 // Round plan: chunk descriptors for draft step 0 (pending draft tokens,
 // right-aligned in 2 slots), draft steps 1..k-1 and the verify chunk
 // (pending target token + k drafts).
-__global__ void k_spec_plan(SpecDev s) {
+__global__ void k_spec_plan(SpecDev s, int W0, int Wv) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= s.B) return;
-  const int dn = s.d_pend_n[b];
-  s.tok_d0[b * 2 + 0] = dn == 2 ? s.d_pend[b * 2 + 0] : 0;
-  s.tok_d0[b * 2 + 1] = s.d_pend[b * 2 + dn - 1];
+  const int P = FC_PMAX, K = s.k;
+  // draft step 0: the last dn pending tokens, right-aligned in W0 slots
+  // (dn < d_pend_n only for finished rows, whose state no longer changes)
+  const int dfull = s.d_pend_n[b];
+  const int dn = min(dfull, W0);
+  for (int j = 0; j < W0; ++j) {
+    const int src = j - (W0 - dn) + (dfull - dn);
+    s.tok_d0[b * W0 + j] = src >= dfull - dn ? s.d_pend[b * P + src] : 0;
+  }
   s.n_d0[b] = dn;
   const int dl = s.d_len[b];
   s.start_d[b] = dl;
-  for (int i = 1; i < s.k; ++i) s.start_d[i * s.B + b] = dl + dn + i - 1;
+  for (int i = 1; i < K; ++i) s.start_d[i * s.B + b] = dl + dn + i - 1;
   s.ones[b] = 1;
-  s.tok_v[b * (s.k + 1)] = s.t_pend[b * 2];
+  // verify: pending target tokens then the k drafts, right-aligned in Wv slots
+  const int tfull = s.t_pend_n[b];
+  const int tn = min(tfull, Wv - K);
+  for (int j = 0; j < Wv - K; ++j) {
+    const int src = j - (Wv - K - tn) + (tfull - tn);
+    s.tok_v[b * Wv + j] = src >= tfull - tn ? s.t_pend[b * P + src] : 0;
+  }
   s.start_v[b] = s.t_len[b];
-  s.n_v[b] = s.t_pend_n[b] + s.k;
+  s.n_v[b] = tn + K;
 }
 
 // Draft step i: statistics of the draft logits row, proposal d_{i+1}
 // (flaxchat/engine.py:493-499), written where the next chunks read it.
-__global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i) {
+__global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i, int Wv) {
   __shared__ StatSmem sm;
   __shared__ int tok_s;
   const int b = blockIdx.x;
@@ -298,7 +310,7 @@ __global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i) {
   if (threadIdx.x == 0) {
     tok_s = tok;
     s.drafts[b * s.k + i] = tok;
-    s.tok_v[b * (s.k + 1) + 1 + i] = tok;
+    s.tok_v[b * Wv + (Wv - s.k) + i] = tok;
     if (i + 1 < s.k) s.tok_ds[(i + 1) * s.B + b] = tok;
   }
 }
@@ -364,6 +376,7 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
   if (sh_mode < 0) {
     if (tid == 0) {
       res[0] = 0; res[1] = 0; res[2] = -1; res[3] = 4; res[4] = 0;
+      res[5] = s.t_pend_n[b]; res[6] = s.d_pend_n[b];
       s.round[b] += 1;
     }
     return;
@@ -398,20 +411,21 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
     if (G0 + i < s.gen_cap) gen[G0 + i] = emitted[i];
   const int gn = min(G0 + n_emit, s.gen_cap);
   s.gen_n[b] = gn;
+  const int P = FC_PMAX;
   const int tb = s.t_len[b], npt = s.t_pend_n[b], db = s.d_len[b], npd = s.d_pend_n[b];
   if (sh_bonus) {
     const int bonus = emitted[n_emit - 1];
     s.t_len[b] = tb + npt + kp;
-    s.t_pend[b * 2] = bonus;
+    s.t_pend[b * P] = bonus;
     s.t_pend_n[b] = 1;
     if (kp == K) {
       s.d_len[b] = db + npd + K - 1;
-      s.d_pend[b * 2] = s.drafts[b * K + K - 1];
-      s.d_pend[b * 2 + 1] = bonus;
+      s.d_pend[b * P] = s.drafts[b * K + K - 1];
+      s.d_pend[b * P + 1] = bonus;
       s.d_pend_n[b] = 2;
     } else {
       s.d_len[b] = db + npd + kp;
-      s.d_pend[b * 2] = bonus;
+      s.d_pend[b * P] = bonus;
       s.d_pend_n[b] = 1;
     }
     if (sh_rej >= 0) {  // rejected last draft: caches keep it, output has the correction
@@ -420,25 +434,34 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
       s.d_dirty[b] = min(s.d_dirty[b], pos);
     }
   } else {
+    // roll back to the accept point, or to the stale entry if earlier; the
+    // tokens from there on are fed again next round (the reference
+    // re-prefills both models from scratch here, engine.py:593-606)
     const int a = sh_acc;
     const int t_new = min(s.t_dirty[b], tb + npt + a - 1);
     const int d_new = min(s.d_dirty[b], db + npd + a - 1);
-    s.t_len[b] = t_new;
-    s.d_len[b] = d_new;
     s.t_dirty[b] = BIG_POS;
     s.d_dirty[b] = BIG_POS;
-    s.t_pend[b * 2] = gen[gn - 1];
-    s.t_pend_n[b] = 1;
-    if (gn - t_new != 1) flags |= 1;  // host feeds gen[t_new, gn-1) then sets t_len = gn-1
-    const int dp = gn - d_new;
-    if (dp == 2) {
-      s.d_pend[b * 2] = gen[gn - 2];
-      s.d_pend[b * 2 + 1] = gen[gn - 1];
-      s.d_pend_n[b] = 2;
+    const int tp = gn - t_new, dp = gn - d_new;
+    if (tp <= P) {
+      s.t_len[b] = t_new;
+      for (int i = 0; i < tp; ++i) s.t_pend[b * P + i] = gen[t_new + i];
+      s.t_pend_n[b] = tp;
+    } else {  // host feeds gen[t_new, gn-1) then sets t_len = gn-1
+      s.t_len[b] = t_new;
+      s.t_pend[b * P] = gen[gn - 1];
+      s.t_pend_n[b] = 1;
+      flags |= 1;
+    }
+    if (dp <= P) {
+      s.d_len[b] = d_new;
+      for (int i = 0; i < dp; ++i) s.d_pend[b * P + i] = gen[d_new + i];
+      s.d_pend_n[b] = dp;
     } else {
-      s.d_pend[b * 2] = gen[gn - 1];
+      s.d_len[b] = d_new;
+      s.d_pend[b * P] = gen[gn - 1];
       s.d_pend_n[b] = 1;
-      if (dp != 1) flags |= 2;
+      flags |= 2;
     }
   }
   if (gn - s.prompt_len[b] >= s.max_tokens) flags |= 4;
@@ -448,6 +471,8 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
   res[2] = sh_rej;
   res[3] = flags;
   res[4] = kp;
+  res[5] = s.t_pend_n[b];
+  res[6] = s.d_pend_n[b];
   for (int i = 0; i < n_emit && i < FC_RES_STRIDE - 8; ++i) res[8 + i] = emitted[i];
 }
 
@@ -459,7 +484,8 @@ static int check_spec(const fc_spec_state* st) {
   return FC_OK;
 }
 
-extern "C" int32_t fc_spec_accept(const fc_spec_state* st, void* stream) {
+extern "C" int32_t fc_spec_accept(const fc_spec_state* st, int32_t w_verify, void* stream) {
+  (void)w_verify;
   int rc = check_spec(st);
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
@@ -473,8 +499,8 @@ extern "C" int32_t fc_spec_accept(const fc_spec_state* st, void* stream) {
 }
 
 extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache, const fc_model* draft,
-                                 const fc_cache* dcache, const fc_spec_state* st, void* work, int64_t work_bytes,
-                                 void* stream) {
+                                 const fc_cache* dcache, const fc_spec_state* st, int32_t w_draft, int32_t w_verify,
+                                 void* work, int64_t work_bytes, void* stream) {
   int rc = check_spec(st);
   if (rc) return rc;
   FC_CHECK_ARG(target && draft && tcache && dcache, "models / caches");
@@ -483,12 +509,14 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
   hipStream_t s = (hipStream_t)stream;
   SpecDev d = to_dev(st);
   const int B = st->batch, K = st->k, V = st->vocab;
-  hipLaunchKernelGGL(k_spec_plan, dim3((B + 255) / 256), dim3(256), 0, s, d);
+  FC_CHECK_ARG(w_draft >= 1 && w_draft <= FC_PMAX, "w_draft must be in [1, FC_PMAX]");
+  FC_CHECK_ARG(w_verify >= K + 1 && w_verify <= FC_PMAX + K, "w_verify must be in [k+1, FC_PMAX+k]");
+  hipLaunchKernelGGL(k_spec_plan, dim3((B + 255) / 256), dim3(256), 0, s, d, w_draft, w_verify);
   FC_LAUNCH_CHECK();
   for (int i = 0; i < K; ++i) {
     fc_chunk ch{};
     if (i == 0) {
-      ch.W = 2;
+      ch.W = w_draft;
       ch.tokens = st->tok_d0;
       ch.start = st->start_d;
       ch.nvalid = st->n_d0;
@@ -503,11 +531,11 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
     ch.logits_stride = (int64_t)K * V;
     rc = fc_forward(draft, dcache, &ch, work, work_bytes, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i);
+    hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i, w_verify);
     FC_LAUNCH_CHECK();
   }
   fc_chunk vch{};
-  vch.W = K + 1;
+  vch.W = w_verify;
   vch.tokens = st->tok_v;
   vch.start = st->start_v;
   vch.nvalid = st->n_v;
@@ -516,7 +544,7 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
   vch.logits_stride = (int64_t)(K + 1) * V;
   rc = fc_forward(target, tcache, &vch, work, work_bytes, stream);
   if (rc) return rc;
-  return fc_spec_accept(st, stream);
+  return fc_spec_accept(st, w_verify, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import FcSpecState, FcRowstat, RES_STRIDE, check, lib
+from ._lib import FcSpecState, FcRowstat, PMAX, RES_STRIDE, check, lib
 from .runtime import DeviceCache, DeviceModel, Workspace, default_device, forward_chunk, prefill_rows
 
 _BIG_POS = 0x3FFFFFFF
@@ -137,24 +137,26 @@ class SpecSession:
             self.dcache = DeviceCache(draft, B, self.cap)
             z = lambda *s: torch.zeros(*s, **i32)
             self.bufs = dict(
-                t_len=z(B), d_len=z(B), t_pend=z(B, 2), d_pend=z(B, 2), t_pend_n=z(B), d_pend_n=z(B),
+                t_len=z(B), d_len=z(B), t_pend=z(B, PMAX), d_pend=z(B, PMAX), t_pend_n=z(B), d_pend_n=z(B),
                 t_dirty=torch.full((B,), _BIG_POS, **i32), d_dirty=torch.full((B,), _BIG_POS, **i32),
                 gen=z(B, self.gen_cap), gen_n=z(B), prompt_len=z(B), round=z(B), result=z(B, RES_STRIDE),
-                tok_d0=z(B, 2), n_d0=z(B), start_d=z(k, B), tok_ds=z(k, B), ones=torch.ones(B, **i32),
-                tok_v=z(B, k + 1), start_v=z(B), n_v=z(B), drafts=z(B, k),
+                tok_d0=z(B, PMAX), n_d0=z(B), start_d=z(k, B), tok_ds=z(k, B), ones=torch.ones(B, **i32),
+                tok_v=z(B, PMAX + k), start_v=z(B), n_v=z(B), drafts=z(B, k),
                 q_logits=torch.zeros(B, k, V, dtype=torch.float32, device=dev),
                 p_logits=torch.zeros(B, k + 1, V, dtype=torch.float32, device=dev),
                 q_stats=torch.zeros(B * k * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev),
                 p_stats=torch.zeros(B * (k + 1) * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev))
         self.state = FcSpecState(B, k, self.max_tokens, self.gen_cap, V, self.temperature, self.top_k, self.seed,
                                  *[self.bufs[n].data_ptr() for n in _lib._SPEC_PTRS])
-        self.ws = Workspace(dev)          # captured by the round graph: never reallocated after capture
+        self.ws = Workspace(dev)          # captured by the round graphs: never reallocated after capture
         self.ws_catchup = Workspace(dev)  # prefill / catch-up
         nb = max(lib().fc_forward_workspace_bytes(ctypes.byref(m.desc), B, w, w)
-                 for m, w in ((target, k + 1), (draft, 2)))
+                 for m, w in ((target, PMAX + k), (draft, PMAX)))
         with torch.cuda.stream(self.stream):
             self.ws.get(nb)
-        self.graph = None
+        self.graphs = {}                  # (draft chunk width, verify width) -> graph exec
+        self.seen = set()
+        self.w_draft, self.w_verify = 1, k + 1
         self.res_h = _Pinned(self.bufs["result"])
         self.rounds = 0
         self.accept_hist = []
@@ -170,7 +172,7 @@ class SpecSession:
             gen = np.zeros((self.B, self.gen_cap), np.int32)
             for i, r in enumerate(self.rows):
                 gen[i, :len(r)] = r
-            pend = np.zeros((self.B, 2), np.int32)
+            pend = np.zeros((self.B, PMAX), np.int32)
             pend[:, 0] = last
             dev = self.dev
             b["t_len"].copy_(torch.from_numpy(P - 1))
@@ -183,30 +185,35 @@ class SpecSession:
             b["gen_n"].copy_(torch.from_numpy(P))
             b["prompt_len"].copy_(torch.from_numpy(P))
 
-    def _round_call(self):
+    def _round_call(self, w0, wv):
         buf = self.ws.buf
         check(lib().fc_spec_round(ctypes.byref(self.T.desc), ctypes.byref(self.tcache.desc),
                                   ctypes.byref(self.Dm.desc), ctypes.byref(self.dcache.desc),
-                                  ctypes.byref(self.state), buf.data_ptr(), buf.numel(),
+                                  ctypes.byref(self.state), w0, wv, buf.data_ptr(), buf.numel(),
                                   self.stream.cuda_stream), "fc_spec_round")
 
     def launch_round(self):
+        """One round with the current chunk widths: replay its graph, capture
+        it on the second use of these widths, or run it eagerly."""
         s = self.stream.cuda_stream
-        if self.graph is not None:
-            check(lib().fc_graph_launch(self.graph, s), "fc_graph_launch")
+        key = (self.w_draft, self.w_verify)
+        ex = self.graphs.get(key)
+        if ex is not None:
+            check(lib().fc_graph_launch(ex, s), "fc_graph_launch")
             return
-        if self.use_graph and self.rounds >= 1:
+        if self.use_graph and key in self.seen:
             check(lib().fc_graph_begin(s), "fc_graph_begin")
             try:
-                self._round_call()
+                self._round_call(*key)
             finally:
                 ex = ctypes.c_void_p()
                 rc = lib().fc_graph_end(s, ctypes.byref(ex))
             check(rc, "fc_graph_end")
-            self.graph = ex
-            check(lib().fc_graph_launch(self.graph, s), "fc_graph_launch")
+            self.graphs[key] = ex
+            check(lib().fc_graph_launch(ex, s), "fc_graph_launch")
             return
-        self._round_call()
+        self.seen.add(key)
+        self._round_call(*key)
 
     def _catch_up(self, flags):
         """Rows whose rollback point lies before the last emitted token (after
@@ -248,6 +255,12 @@ class SpecSession:
                 self.accept_hist.append(res[active, 1].copy())
             if (flags & 3).any():
                 self._catch_up(flags)
+            live = (flags & 4) == 0
+            if live.any():
+                t_pend = np.where(flags & 1, 1, res[:, 5])[live]
+                d_pend = np.where(flags & 2, 1, res[:, 6])[live]
+                self.w_draft = int(max(1, d_pend.max()))
+                self.w_verify = int(t_pend.max()) + self.k
             if (flags & 4).all():
                 break
             if max_rounds is not None and n >= max_rounds:
@@ -265,9 +278,9 @@ class SpecSession:
         return int(np.minimum(gen_n - P, self.max_tokens).sum())
 
     def close(self):
-        if self.graph is not None:
-            lib().fc_graph_destroy(self.graph)
-            self.graph = None
+        for ex in self.graphs.values():
+            lib().fc_graph_destroy(ex)
+        self.graphs = {}
 
     def __del__(self):
         try:

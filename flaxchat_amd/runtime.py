@@ -204,7 +204,8 @@ class DeviceCache:
 
 
 class Workspace:
-    """Growable device scratch for fc_forward."""
+    """Growable, zero-filled device scratch (the library keeps the split-K
+    counters it holds at zero between calls)."""
 
     def __init__(self, device):
         self.device = device
@@ -212,7 +213,7 @@ class Workspace:
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.empty(int(nbytes), dtype=torch.uint8, device=self.device)
+            self.buf = torch.zeros(int(nbytes), dtype=torch.uint8, device=self.device)
         return self.buf
 
 

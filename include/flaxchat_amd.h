@@ -106,7 +106,7 @@ typedef struct fc_spec_state {
   int32_t top_k;          /* <= 0: off                                         */
   uint64_t seed;
   int32_t* t_len;  int32_t* d_len;       /* [B] cache lengths                  */
-  int32_t* t_pend; int32_t* d_pend;      /* [B][2] pending tokens              */
+  int32_t* t_pend; int32_t* d_pend;      /* [B][FC_PMAX] pending tokens        */
   int32_t* t_pend_n; int32_t* d_pend_n;  /* [B]                                */
   int32_t* t_dirty; int32_t* d_dirty;    /* [B] earliest fed != emitted pos    */
   int32_t* gen;    int32_t* gen_n;       /* [B][gen_cap] tokens incl. prompt   */
@@ -114,12 +114,12 @@ typedef struct fc_spec_state {
   int32_t* round;                        /* [B] round counter (Philox)         */
   int32_t* result;                       /* [B][FC_RES_STRIDE]                 */
   /* per-round scratch */
-  int32_t* tok_d0;   /* [B][2]          draft chunk 0 tokens                   */
+  int32_t* tok_d0;   /* [B][FC_PMAX]    draft chunk 0 tokens                   */
   int32_t* n_d0;     /* [B]                                                    */
   int32_t* start_d;  /* [k][B]          draft step start positions             */
   int32_t* tok_ds;   /* [k][B]          draft step tokens (steps 1..k-1)       */
   int32_t* ones;     /* [B]             all 1                                  */
-  int32_t* tok_v;    /* [B][k+1]        verify chunk tokens                    */
+  int32_t* tok_v;    /* [B][FC_PMAX+k]  verify chunk tokens                    */
   int32_t* start_v;  /* [B]                                                    */
   int32_t* n_v;      /* [B]                                                    */
   int32_t* drafts;   /* [B][k]                                                 */
@@ -130,9 +130,14 @@ typedef struct fc_spec_state {
 } fc_spec_state;
 
 #define FC_RES_STRIDE 40
-/* result row layout: [0] n_emitted this round, [1] accepted, [2] rejected
- * index or -1, [3] flags (bit0 target needs catch-up, bit1 draft needs
- * catch-up, bit2 row finished), [4] k', [8..8+k+1] emitted tokens. */
+#define FC_PMAX 16
+/* Tokens a model still has to be fed (fed next round ahead of the drafts):
+ * normally 1 (target) or 1-2 (draft); after a rejection that rolls back past
+ * a stale cache entry, up to FC_PMAX. Result row layout: [0] n_emitted this
+ * round, [1] accepted, [2] rejected index or -1, [3] flags (bit0 target
+ * needs catch-up, bit1 draft needs catch-up: more than FC_PMAX pending; bit2
+ * row finished), [4] k', [5] target pending count, [6] draft pending count,
+ * [8..8+k+1] emitted tokens. */
 
 const char* fc_last_error(void);
 int32_t fc_version(void);
@@ -177,11 +182,14 @@ int32_t fc_row_stats(const float* logits, int32_t rows, int32_t V, float tempera
  * verify, accept/reject with residual resampling, bonus, bookkeeping. */
 int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
                       const fc_model* draft, const fc_cache* dcache,
-                      const fc_spec_state* st, void* work, int64_t work_bytes, void* stream);
+                      const fc_spec_state* st, int32_t w_draft, int32_t w_verify,
+                      void* work, int64_t work_bytes, void* stream);
+/* w_draft >= every active row's draft pending count (chunk width of draft
+ * step 0); w_verify >= every active row's target pending count + k. */
 
 /* Accept/reject step alone on given logits (flaxchat/engine.py:525-592);
  * updates the state like fc_spec_round does. */
-int32_t fc_spec_accept(const fc_spec_state* st, void* stream);
+int32_t fc_spec_accept(const fc_spec_state* st, int32_t w_verify, void* stream);
 
 /* generate_fast sampling step (flaxchat/engine.py:308-324, 343-368): for
  * rows with !done[b] && pos[b] < max_pos[b], sample from logits row b,

@@ -44,7 +44,7 @@ def test_argument_errors_are_status_codes():
     rc = L.fc_attention(None, None, None, None, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None, 0, None)
     assert rc == -1
     st = _lib.FcSpecState()
-    assert L.fc_spec_accept(ctypes.byref(st), None) == -1
+    assert L.fc_spec_accept(ctypes.byref(st), 5, None) == -1
 
 
 def test_struct_layout_matches_c(tmp_path):

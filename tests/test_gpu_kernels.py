@@ -42,10 +42,15 @@ def bf(x):
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 @pytest.mark.parametrize("M", [1, 3, 5, 16, 32, 64, 100, 224, 300])
 @pytest.mark.parametrize("epi", [0, 1, 2, 4])
-def test_gemm_parity(dtype, M, epi):
-    _say(f"gemm dtype={dtype} M={M} epi={epi}")
+@pytest.mark.parametrize("NK", [(256, 384), (1536, 6144)])
+def test_gemm_parity(dtype, M, epi, NK):
+    """Small and model-sized shapes through every kernel family (VALU GEMV,
+    streaming MFMA, LDS-tiled MFMA with 64-row and full-M tiles)."""
+    _say(f"gemm dtype={dtype} M={M} epi={epi} NK={NK}")
     rng = np.random.default_rng(M * 10 + epi)
-    N, K = 256, 384
+    N, K = NK
+    if N * K > 1e6 and (epi in (1, 4) or (dtype == "fp32" and M > 64)):
+        pytest.skip("covered by the small shape; keeps the run short")
     A = rng.standard_normal((M, K)).astype(np.float32)
     W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
     if dtype == "bf16":
