@@ -49,6 +49,11 @@ CONFIGS = {
                   window_pattern="SSSL", short_window=2048), 4, 128, 6144, 1024, 8, 0.0, 3),
 }
 HBM_PEAK_GBS = 8000.0
+# HBM bytes / algorithmic bytes of the verify attention (k_attn_mfma +
+# k_attn_combine), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
+# `bench.py --roofline-only`, each scaled by the counter's reading for a
+# 256 MiB copy (FETCH_SIZE x2.0, WRITE_SIZE x1.0); see profiles/.
+ATTN_TRAFFIC_RATIO = 1.14
 
 
 def attention_roofline(sess, n_iter=20):
@@ -118,8 +123,8 @@ def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0):
     ht = to_host(dm_t)
     hd = to_host(dm_d)
     V = dm_t.V
-    prompt = np.random.default_rng(seed).integers(0, V, 16).tolist()
-    new = 6
+    prompt = np.random.default_rng(seed).integers(0, V, 64).tolist()
+    new = 48
     t0 = time.perf_counter()
     out = spec_literal(ht, hd, prompt, max_tokens=new, temperature=temperature, top_k=None, seed=seed,
                        draft_steps=k)
@@ -127,7 +132,7 @@ def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0):
     return {"value": round((len(out) - len(prompt)) / dt, 4), "unit": "tokens/s", "cores": int(cores),
             "kind": "port",
             "sample": f"oracle spec_literal (restatement of flaxchat/engine.py:410-608, fp32 numpy) on the "
-                      f"{cfg_name} architecture and weights, batch 1, prompt 16 ids (not the full prompt), "
+                      f"{cfg_name} architecture and weights, batch 1, prompt 64 ids (not the full prompt), "
                       f"{new} new tokens, k={k}, T={temperature}, including prefill; {dt:.1f} s"}
 
 
@@ -141,6 +146,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="prefill + warmup rounds, then only the verify-attention timing and a 256 MiB copy "
+                         "(the counter-calibration kernel); for rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the speculative engine shards over the batch "
@@ -168,6 +176,15 @@ def main():
     print(f"[bench] init {t_pre - t_init:.1f}s prefill {prefill_s:.2f}s ({B}x{P} tokens)", file=sys.stderr, flush=True)
     if args.warmup:
         sess.run(max_rounds=args.warmup)
+    if args.roofline_only:
+        r = attention_roofline(sess)
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=target.device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"verify_attention": r, "copy_bytes": 1 << 28}))
+        return
     done_before = sess.emitted_tokens()
     rounds_before = sess.rounds
     sess.stream.synchronize()
@@ -187,7 +204,8 @@ def main():
     if not args.no_roofline:
         r = attention_roofline(sess)
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
+                "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
                 "kernel": "k_attn_mfma + k_attn_combine (verify, k+1 queries per row)",
                 "per_launch_bytes": int(r["per_launch_bytes"]), "per_launch_us": round(r["per_launch_us"], 2),
                 "S_layer": r["S"], "L_layer": r["L"]}

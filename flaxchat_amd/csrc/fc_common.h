@@ -105,8 +105,10 @@ __device__ __forceinline__ u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1
 __device__ __forceinline__ uint32_t pick(const u32x4& r, int i) {
   return i == 0 ? r.x : (i == 1 ? r.y : (i == 2 ? r.z : r.w));
 }
-// u in (0, 1) for Gumbel noise; u in [0, 1) for accept tests.
-__device__ __forceinline__ float u_open(uint32_t bits) { return ((float)(bits >> 8) + 0.5f) * 5.9604644775390625e-8f; }
+// u in (0, 1) for Gumbel noise: 23 random bits plus one half, exact in fp32
+// (with 24 bits, (2^24 - 1) + 0.5 rounds to 2^24 and u would reach 1.0);
+// u in [0, 1) for accept tests.
+__device__ __forceinline__ float u_open(uint32_t bits) { return ((float)(bits >> 9) + 0.5f) * 1.1920928955078125e-7f; }
 __device__ __forceinline__ float u_half(uint32_t bits) { return (float)(bits >> 8) * 5.9604644775390625e-8f; }
 
 // ---------------------------------------------------------------------------

@@ -193,3 +193,102 @@ def reference_lambdas(n_layer: int):
     resid = np.array([1.15 - (0.10 * i / den) for i in range(n_layer)], dtype=np.float32)
     x0 = np.array([0.20 - (0.15 * i / den) for i in range(n_layer)], dtype=np.float32)
     return resid, x0
+
+
+# ----------------------------------------------------------------------
+# Loading the reference's parameter tree
+# ----------------------------------------------------------------------
+def _get(d, *keys):
+    for k in keys:
+        if isinstance(d, dict):
+            if k in d:
+                d = d[k]
+            elif str(k) in d:
+                d = d[str(k)]
+            elif isinstance(k, str) and k.isdigit() and int(k) in d:
+                d = d[int(k)]
+            else:
+                raise KeyError(f"missing parameter {'/'.join(map(str, keys))}")
+        else:
+            d = d[int(k)]
+    return np.asarray(d, dtype=np.float32)
+
+
+def from_pure_dict(config: GPTConfig, params: dict) -> GPT:
+    """Build the host container from the nested dict the reference exports
+    with `nnx.to_pure_dict(nnx.state(model, nnx.Param))`
+    (flaxchat/scripts/run_tinystories.py:328-345, flaxchat/checkpoint.py:47-66).
+    Block indices may be ints or strings."""
+    L = config.n_layer
+    blocks = []
+    for i in range(L):
+        a = Attention(Linear(_get(params, "blocks", i, "attn", "c_q", "kernel")),
+                      Linear(_get(params, "blocks", i, "attn", "c_k", "kernel")),
+                      Linear(_get(params, "blocks", i, "attn", "c_v", "kernel")),
+                      Linear(_get(params, "blocks", i, "attn", "c_proj", "kernel")))
+        if has_ve(i, L):
+            a.ve_gate = Linear(_get(params, "blocks", i, "attn", "ve_gate", "kernel"))
+        m = MLP(Linear(_get(params, "blocks", i, "mlp", "c_fc", "kernel")),
+                Linear(_get(params, "blocks", i, "mlp", "c_proj", "kernel")))
+        blocks.append(Block(a, m))
+    ves = {str(i): Embed(_get(params, "value_embeds", str(i), "embedding")) for i in range(L) if has_ve(i, L)}
+    lm = None if config.tie_embeddings else Linear(_get(params, "lm_head", "kernel"))
+    return GPT(config, Embed(_get(params, "wte", "embedding")), blocks, lm, _get(params, "resid_lambdas"),
+               _get(params, "x0_lambdas"), Linear(_get(params, "smear_gate", "kernel")),
+               _get(params, "smear_lambda"), _get(params, "backout_lambda"), ves)
+
+
+def to_pure_dict(model: GPT) -> dict:
+    """The inverse of from_pure_dict (reference parameter tree, numpy)."""
+    d = {"wte": {"embedding": model.wte.embedding}, "blocks": {},
+         "resid_lambdas": model.resid_lambdas, "x0_lambdas": model.x0_lambdas,
+         "smear_gate": {"kernel": model.smear_gate.kernel}, "smear_lambda": model.smear_lambda,
+         "backout_lambda": model.backout_lambda,
+         "value_embeds": {k: {"embedding": v.embedding} for k, v in model.value_embeds.items()}}
+    if model.lm_head is not None:
+        d["lm_head"] = {"kernel": model.lm_head.kernel}
+    for i, b in enumerate(model.blocks):
+        attn = {"c_q": {"kernel": b.attn.c_q.kernel}, "c_k": {"kernel": b.attn.c_k.kernel},
+                "c_v": {"kernel": b.attn.c_v.kernel}, "c_proj": {"kernel": b.attn.c_proj.kernel}}
+        if b.attn.ve_gate is not None:
+            attn["ve_gate"] = {"kernel": b.attn.ve_gate.kernel}
+        d["blocks"][i] = {"attn": attn, "mlp": {"c_fc": {"kernel": b.mlp.c_fc.kernel},
+                                                "c_proj": {"kernel": b.mlp.c_proj.kernel}}}
+    return d
+
+
+def save_npz(model: GPT, path: str) -> None:
+    """Flatten the parameter tree to 'a/b/c' keys in an .npz (no pickle)."""
+    flat = {}
+
+    def walk(prefix, node):
+        if isinstance(node, dict):
+            for k, v in node.items():
+                walk(f"{prefix}/{k}" if prefix else str(k), v)
+        else:
+            flat[prefix] = np.asarray(node)
+    walk("", to_pure_dict(model))
+    cfg = model.config
+    flat["__config__"] = np.array([cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head, cfg.n_kv_head,
+                                   cfg.n_embd, int(cfg.tie_embeddings), cfg.short_window or 0], np.int64)
+    flat["__window_pattern__"] = np.frombuffer(cfg.window_pattern.encode(), dtype=np.uint8)
+    np.savez(path, **flat)
+
+
+def load_npz(path: str) -> GPT:
+    """Load a model saved by save_npz (numpy.load without pickle)."""
+    z = np.load(path, allow_pickle=False)
+    c = z["__config__"].tolist()
+    cfg = GPTConfig(sequence_len=c[0], vocab_size=c[1], n_layer=c[2], n_head=c[3], n_kv_head=c[4], n_embd=c[5],
+                    tie_embeddings=bool(c[6]), short_window=(c[7] or None),
+                    window_pattern=bytes(z["__window_pattern__"]).decode())
+    tree: dict = {}
+    for key in z.files:
+        if key.startswith("__"):
+            continue
+        node = tree
+        parts = key.split("/")
+        for p in parts[:-1]:
+            node = node.setdefault(p, {})
+        node[parts[-1]] = z[key]
+    return from_pure_dict(cfg, tree)

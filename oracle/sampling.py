@@ -15,7 +15,8 @@ generate_fast uses round = step index, slot 0.
 
 A categorical draw is Gumbel-max, like jax.random.categorical:
   argmax_v (log(max(p_v, 1e-10)) + G_v),  G_v = -log(-log(u_v)),
-  u_v = ((bits >> 8) + 0.5) * 2^-24 from word v % 4 of counter (v // 4, ...).
+  u_v = ((bits >> 9) + 0.5) * 2^-23 from word v % 4 of counter (v // 4, ...)
+  (23 bits keep u < 1 exactly in fp32).
 An accept uniform is (bits >> 8) * 2^-24 from word 0 of counter (0, ...).
 """
 
@@ -72,7 +73,7 @@ def vocab_bits(V: int, seed: int, row: int, rnd: int, slot: int):
 
 def gumbel(V, seed, row, rnd, slot):
     bits = vocab_bits(V, seed, row, rnd, slot)
-    u = (((bits >> U32(8)).astype(F32) + F32(0.5)) * F32(2.0 ** -24)).astype(F32)
+    u = (((bits >> U32(9)).astype(F32) + F32(0.5)) * F32(2.0 ** -23)).astype(F32)
     return (-np.log(-np.log(u))).astype(F32)
 
 

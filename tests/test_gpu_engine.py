@@ -193,3 +193,17 @@ def test_spec_sampling_chi_square(tiny_pair):
     stat, pval = chisquare(obs, ex * obs.sum() / ex.sum())
     _say(f"chi-square {stat:.1f} p={pval:.3g} bins={len(obs)}")
     assert pval > 1e-4
+
+
+@pytest.mark.parametrize("case_idx", [0, 1, 2])
+def test_golden_cfg1_streams(case_idx):
+    """BASELINE configs[0] streams (greedy and sampled) from the committed
+    oracle fixture, reproduced by the fp32 engine."""
+    import json, os
+    from tests.golden.make_golden import cfg1_models
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "cfg1_oracle.json")))
+    tgt, draft = cfg1_models()
+    c = g["cases"][case_idx]
+    got = generate_speculative(tgt, draft, g["prompt"], max_tokens=64, temperature=c["temperature"],
+                               top_k=c["top_k"], seed=c["seed"], draft_steps=c["draft_steps"], dtype="fp32")
+    assert got == c["tokens"]

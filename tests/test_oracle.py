@@ -309,3 +309,40 @@ def test_fast_eos_first_token():
     first = generate_fast(t, prompt, max_tokens=4, temperature=0, eos_token=-1)[3]
     out = generate_fast(t, prompt, max_tokens=4, temperature=0, eos_token=first)
     assert out == prompt + [first]
+
+
+def test_parameter_tree_round_trip(tmp_path):
+    """from_pure_dict / to_pure_dict / npz keep every parameter (the tree the
+    reference exports with nnx.to_pure_dict, scripts/run_tinystories.py:328-345)."""
+    from flaxchat_amd.gpt import from_pure_dict, load_npz, save_npz, to_pure_dict
+    t, _ = _tiny(7)
+    t2 = from_pure_dict(t.config, to_pure_dict(t))
+    save_npz(t2, tmp_path / "m.npz")
+    t3 = load_npz(str(tmp_path / "m.npz"))
+    toks = [3, 1, 4, 1, 5]
+    a = OracleModel(t).prefill(toks, OracleModel(t).new_state(8))
+    b = OracleModel(t3).prefill(toks, OracleModel(t3).new_state(8))
+    np.testing.assert_array_equal(a, b)
+
+
+def test_golden_cfg1_greedy_stream():
+    """The oracle still produces the committed BASELINE configs[0] greedy stream."""
+    import json, os
+    from tests.golden.make_golden import cfg1_models
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "cfg1_oracle.json")))
+    tgt, draft = cfg1_models()
+    case = g["cases"][0]
+    assert case["temperature"] == 0.0
+    got = spec_literal(tgt, draft, g["prompt"], max_tokens=64, temperature=0.0, top_k=case["top_k"],
+                       seed=case["seed"], draft_steps=4)
+    assert got == case["tokens"]
+
+
+def test_gumbel_uniform_strictly_inside_unit_interval():
+    """The largest and smallest 32-bit draws map strictly inside (0, 1), so
+    every Gumbel value is finite (24 bits + 0.5 would round to 1.0)."""
+    bits = np.array([0, 1, 0xFFFFFFFF, 0xFFFFFF00, 0xFFFFFE00], np.uint32)
+    u = (((bits >> np.uint32(9)).astype(np.float32) + np.float32(0.5)) * np.float32(2.0 ** -23)).astype(np.float32)
+    assert np.all(u > 0) and np.all(u < 1)
+    g = S.gumbel(1 << 16, 2, 0, 0, 0)
+    assert np.all(np.isfinite(g))
