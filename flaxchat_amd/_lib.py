@@ -58,13 +58,13 @@ _SPEC_PTRS = ["t_len", "d_len", "t_pend", "d_pend", "t_pend_n", "d_pend_n", "t_d
 class FcSpecState(Structure):
     _fields_ = ([("batch", c_int32), ("k", c_int32), ("max_tokens", c_int32), ("gen_cap", c_int32),
                  ("vocab", c_int32), ("temperature", c_float), ("top_k", c_int32), ("seed", c_uint64)]
-                + [(n, c_void_p) for n in _SPEC_PTRS])
+                + [(n, c_void_p) for n in _SPEC_PTRS] + [("part", c_void_p), ("part_bytes", c_int64)])
 
 
 EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forward", "fc_gemm",
            "fc_attention_workspace_bytes", "fc_attention", "fc_row_stats", "fc_spec_round",
-           "fc_spec_accept", "fc_fast_sample", "fc_graph_begin", "fc_graph_end", "fc_graph_launch",
-           "fc_graph_destroy"]
+           "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_graph_begin", "fc_graph_end",
+           "fc_graph_launch", "fc_graph_destroy"]
 
 _lib = None
 
@@ -90,6 +90,8 @@ def _declare(L):
     L.fc_spec_round.restype = i32
     L.fc_spec_accept.argtypes = [POINTER(FcSpecState), i32, vp]
     L.fc_spec_accept.restype = i32
+    L.fc_spec_part_bytes.argtypes = [i32, i32, i32]
+    L.fc_spec_part_bytes.restype = i64
     L.fc_fast_sample.argtypes = [vp, i32, i32, f32, i32, c_uint64, i32, vp, i32, vp, vp, vp, vp, vp, vp, vp]
     L.fc_fast_sample.restype = i32
     L.fc_graph_begin.argtypes = [vp]

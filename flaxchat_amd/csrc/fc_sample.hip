@@ -315,95 +315,13 @@ __global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i, int Wv)
   }
 }
 
-// Accept/reject (flaxchat/engine.py:525-592) and the rollback bookkeeping.
-__global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
-  __shared__ StatSmem sm;
-  __shared__ int sh_mode, sh_row, sh_n, sh_acc, sh_rej, sh_bonus, sh_kp;
-  __shared__ int emitted[64];
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const int K = s.k, V = s.V;
-  const bool greedy = !(s.T > 0.f);
+// The rollback state machine after one accept/reject pass: append the
+// emitted tokens, move the cache lengths and pending tokens of both models,
+// and fill the row's result record.
+__device__ void bookkeep(const SpecDev& s, int b, const int* emitted, int n_emit, int acc, int rej,
+                         int bonus_emitted, int kp, int rnd) {
   int* res = s.result + (int64_t)b * FC_RES_STRIDE;
-  if (tid == 0) {
-    const int ng = s.gen_n[b] - s.prompt_len[b];
-    const int kp = min(K, s.max_tokens - ng);
-    sh_kp = kp;
-    sh_mode = -1;
-    sh_n = 0;
-    sh_acc = 0;
-    sh_rej = -1;
-    sh_bonus = 0;
-    if (kp > 0) {
-      sh_mode = 0;
-      int acc = 0, n = 0;
-      for (int i = 0; i < kp; ++i) {
-        const int dt = s.drafts[b * K + i];
-        const fc_rowstat ps = s.p_stats[b * (K + 1) + i];
-        if (greedy) {
-          const int am = ps.argmax;
-          emitted[n++] = am == dt ? dt : am;
-          ++acc;
-          if (am != dt) { sh_rej = i; break; }
-        } else {
-          const fc_rowstat qs = s.q_stats[b * K + i];
-          const float* zp = s.p_logits + ((int64_t)b * (K + 1) + i) * V;
-          const float* zq = s.q_logits + ((int64_t)b * K + i) * V;
-          const float pm = prob_at(zp, ps, s.T, dt);
-          const float pd = prob_at(zq, qs, s.T, dt);
-          if (pd == 0.f) {
-            sh_mode = 1; sh_row = i; ++acc; sh_rej = i;
-            break;
-          }
-          const double ap = fmin(1.0, (double)pm / (double)pd);
-          const u32x4 r = philox4x32_10(u32x4{0u, (uint32_t)b, (uint32_t)s.round[b], (uint32_t)(SLOT_ACCEPT + i)},
-                                        (uint32_t)s.seed, (uint32_t)(s.seed >> 32));
-          const double u = (double)u_half(r.x);
-          if (u < ap) {
-            emitted[n++] = dt;
-            ++acc;
-          } else {
-            sh_mode = 2; sh_row = i; ++acc; sh_rej = i;
-            break;
-          }
-        }
-      }
-      sh_n = n;
-      sh_acc = acc;
-      sh_bonus = acc == kp;
-    }
-  }
-  __syncthreads();
-  if (sh_mode < 0) {
-    if (tid == 0) {
-      res[0] = 0; res[1] = 0; res[2] = -1; res[3] = 4; res[4] = 0;
-      res[5] = s.t_pend_n[b]; res[6] = s.d_pend_n[b];
-      s.round[b] += 1;
-    }
-    return;
-  }
-  const int rnd = s.round[b];
-  if (sh_mode > 0) {
-    const int i = sh_row;
-    const fc_rowstat ps = s.p_stats[b * (K + 1) + i];
-    const fc_rowstat qs = s.q_stats[b * K + i];
-    const int c = block_draw(s.p_logits + ((int64_t)b * (K + 1) + i) * V, ps, s.q_logits + ((int64_t)b * K + i) * V,
-                             qs, sh_mode == 2 ? 1 : 0, s.T, V, s.seed, b, rnd, SLOT_REJECT, sm);
-    if (tid == 0) emitted[sh_n++] = c;
-    __syncthreads();
-  }
-  const int kp = sh_kp;
-  if (sh_bonus) {
-    const fc_rowstat ps = s.p_stats[b * (K + 1) + kp];
-    int bt;
-    if (greedy) bt = ps.argmax;
-    else bt = block_draw(s.p_logits + ((int64_t)b * (K + 1) + kp) * V, ps, nullptr, ps, 0, s.T, V, s.seed, b, rnd,
-                         SLOT_BONUS, sm);
-    if (tid == 0) emitted[sh_n++] = bt;
-    __syncthreads();
-  }
-  if (tid != 0) return;
-  // ---- bookkeeping (the rollback state machine) ----
-  const int n_emit = sh_n;
+  const int K = s.k;
   const int G0 = s.gen_n[b];
   int* gen = s.gen + (int64_t)b * s.gen_cap;
   int flags = 0;
@@ -413,7 +331,7 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
   s.gen_n[b] = gn;
   const int P = FC_PMAX;
   const int tb = s.t_len[b], npt = s.t_pend_n[b], db = s.d_len[b], npd = s.d_pend_n[b];
-  if (sh_bonus) {
+  if (bonus_emitted) {
     const int bonus = emitted[n_emit - 1];
     s.t_len[b] = tb + npt + kp;
     s.t_pend[b * P] = bonus;
@@ -428,7 +346,7 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
       s.d_pend[b * P] = bonus;
       s.d_pend_n[b] = 1;
     }
-    if (sh_rej >= 0) {  // rejected last draft: caches keep it, output has the correction
+    if (rej >= 0) {  // rejected last draft: caches keep it, output has the correction
       const int pos = G0 + kp - 1;
       s.t_dirty[b] = min(s.t_dirty[b], pos);
       s.d_dirty[b] = min(s.d_dirty[b], pos);
@@ -437,7 +355,7 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
     // roll back to the accept point, or to the stale entry if earlier; the
     // tokens from there on are fed again next round (the reference
     // re-prefills both models from scratch here, engine.py:593-606)
-    const int a = sh_acc;
+    const int a = acc;
     const int t_new = min(s.t_dirty[b], tb + npt + a - 1);
     const int d_new = min(s.d_dirty[b], db + npd + a - 1);
     s.t_dirty[b] = BIG_POS;
@@ -467,8 +385,8 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
   if (gn - s.prompt_len[b] >= s.max_tokens) flags |= 4;
   s.round[b] = rnd + 1;
   res[0] = n_emit;
-  res[1] = sh_acc;
-  res[2] = sh_rej;
+  res[1] = acc;
+  res[2] = rej;
   res[3] = flags;
   res[4] = kp;
   res[5] = s.t_pend_n[b];
@@ -476,11 +394,521 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
   for (int i = 0; i < n_emit && i < FC_RES_STRIDE - 8; ++i) res[8 + i] = emitted[i];
 }
 
+// Accept/reject decision of one row (flaxchat/engine.py:525-592) from the
+// target row statistics `ps` (k+1 rows) and the draft statistics: accepted
+// drafts, the greedy correction and greedy bonus go to `emitted`; a sampled
+// rejection or bonus is left as a draw request (mode / bonus_draw).
+struct Decision {
+  int mode;        // -1 finished row, 0 no rejection draw, 1 draw from p, 2 from the residual
+  int row;         // verify row of the rejection draw
+  int n, acc, rej, bonus, kp;
+  int bonus_draw;  // the bonus token is still to be drawn (sampling)
+  int emitted[24];
+};
+static_assert(sizeof(Decision) == 32 * sizeof(int), "Decision layout");
+
+__device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& d) {
+  const int K = s.k, V = s.V;
+  const bool greedy = !(s.T > 0.f);
+  const int ng = s.gen_n[b] - s.prompt_len[b];
+  const int kp = min(K, s.max_tokens - ng);
+  d.kp = kp;
+  d.mode = -1;
+  d.row = 0;
+  d.n = 0;
+  d.acc = 0;
+  d.rej = -1;
+  d.bonus = 0;
+  d.bonus_draw = 0;
+  if (kp <= 0) return;
+  d.mode = 0;
+  int acc = 0, n = 0;
+  for (int i = 0; i < kp; ++i) {
+    const int dt = s.drafts[b * K + i];
+    if (greedy) {
+      const int am = ps[i].argmax;
+      d.emitted[n++] = am;
+      ++acc;
+      if (am != dt) { d.rej = i; break; }
+    } else {
+      const fc_rowstat qs = s.q_stats[b * K + i];
+      const float* zp = s.p_logits + ((int64_t)b * (K + 1) + i) * V;
+      const float* zq = s.q_logits + ((int64_t)b * K + i) * V;
+      const float pm = prob_at(zp, ps[i], s.T, dt);
+      const float pd = prob_at(zq, qs, s.T, dt);
+      if (pd == 0.f) {
+        d.mode = 1; d.row = i; ++acc; d.rej = i;
+        break;
+      }
+      const double ap = fmin(1.0, (double)pm / (double)pd);
+      const u32x4 r = philox4x32_10(u32x4{0u, (uint32_t)b, (uint32_t)s.round[b], (uint32_t)(SLOT_ACCEPT + i)},
+                                    (uint32_t)s.seed, (uint32_t)(s.seed >> 32));
+      const double u = (double)u_half(r.x);
+      if (u < ap) {
+        d.emitted[n++] = dt;
+        ++acc;
+      } else {
+        d.mode = 2; d.row = i; ++acc; d.rej = i;
+        break;
+      }
+    }
+  }
+  d.acc = acc;
+  d.bonus = acc == kp;
+  if (d.bonus) {
+    if (greedy) d.emitted[n++] = ps[kp].argmax;
+    else d.bonus_draw = 1;
+  }
+  d.n = n;
+}
+
+__device__ void finished_row(const SpecDev& s, int b) {
+  int* res = s.result + (int64_t)b * FC_RES_STRIDE;
+  res[0] = 0; res[1] = 0; res[2] = -1; res[3] = 4; res[4] = 0;
+  res[5] = s.t_pend_n[b]; res[6] = s.d_pend_n[b];
+  s.round[b] += 1;
+}
+
+// Accept/reject with the top-k filter (one workgroup per row): decision,
+// rejection / bonus draws, rollback bookkeeping.
+__global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
+  __shared__ StatSmem sm;
+  __shared__ Decision d;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int K = s.k, V = s.V;
+  if (tid == 0) decide(s, b, s.p_stats + b * (K + 1), d);
+  __syncthreads();
+  if (d.mode < 0) {
+    if (tid == 0) finished_row(s, b);
+    return;
+  }
+  const int rnd = s.round[b];
+  if (d.mode > 0) {
+    const int i = d.row;
+    const fc_rowstat ps = s.p_stats[b * (K + 1) + i];
+    const fc_rowstat qs = s.q_stats[b * K + i];
+    const int c = block_draw(s.p_logits + ((int64_t)b * (K + 1) + i) * V, ps, s.q_logits + ((int64_t)b * K + i) * V,
+                             qs, d.mode == 2 ? 1 : 0, s.T, V, s.seed, b, rnd, SLOT_REJECT, sm);
+    if (tid == 0) d.emitted[d.n++] = c;
+    __syncthreads();
+  }
+  if (d.bonus_draw) {
+    const int kp = d.kp;
+    const fc_rowstat ps = s.p_stats[b * (K + 1) + kp];
+    const int bt = block_draw(s.p_logits + ((int64_t)b * (K + 1) + kp) * V, ps, nullptr, ps, 0, s.T, V, s.seed, b,
+                              rnd, SLOT_BONUS, sm);
+    if (tid == 0) d.emitted[d.n++] = bt;
+    __syncthreads();
+  }
+  if (tid != 0) return;
+  bookkeep(s, b, d.emitted, d.n, d.acc, d.rej, d.bonus, d.kp, rnd);
+}
+
+// ---------------------------------------------------------------------------
+// Vocab passes without a top-k filter, split over many workgroups: a logits
+// row is cut into chunks of VP_CHUNK * NV entries (one 256-thread workgroup,
+// 4 consecutive entries per thread and sub-block, so one Philox block per
+// thread), each writes a 32-byte partial, and one wave per row merges them.
+//
+// A Gumbel-max draw over log(max(p, 1e-10)) + G with p = exp(x - M) / S,
+// x = z / T, is taken in one pass before M and S are known: per element the
+// score is max(x - C, log 1e-10) + G with C = M + log S, so per chunk it is
+//   max(a_c - (M - m_c + log S), log 1e-10 + g_c),
+// a_c = max(x - m_c + G) (relative to the chunk's max m_c, which keeps the
+// sums small for any T), g_c = max G; the argmax index of each term is kept.
+// ---------------------------------------------------------------------------
+#define VP_THR 256
+#define VP_CHUNK (VP_THR * 4)
+#define VP_MAXWG 2048
+
+struct VPart {  // one chunk of one logits row
+  float zmax; int zarg;  // argmax of z (first index among equals)
+  float m, s;            // max of x = z / T and sum of exp(x - m)
+  float a; int ai;       // max of x - m + G, and its index
+  float g; int gi;       // max of G, and its index
+};
+struct DPart {  // one chunk of a draw from finished row statistics
+  float sc; int si;      // max of log(max(p, 1e-10)) + G
+  float A; int Ai;       // residual: max of log r + G over r = max(p - q, 0) > 0
+  float g; int gi;       // max of G
+  float R; int pad;      // residual: sum of r
+};
+static_assert(sizeof(VPart) == 32 && sizeof(DPart) == 32, "partial layout");
+
+__device__ __forceinline__ float log_floor() { return logf(1e-10f); }
+
+// Four entries e..e+3 of row z (-inf beyond V).
+__device__ __forceinline__ void load4(const float* __restrict__ z, int e, int V, bool vec, float* v) {
+  if (vec && e + 3 < V) {
+    const float4 q = *reinterpret_cast<const float4*>(z + e);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v[w] = e + w < V ? z[e + w] : -INFINITY;
+  }
+}
+
+// Block-wide (value, index) argmax for a VP_THR block; result in thread 0.
+__device__ __forceinline__ void vp_argmax(float& v, int& i, float* redv, int* redi) {
+  block_argmax(v, i, redv, redi);
+}
+
+// Chunk partials of rows r of z0 (row stride `row_stride` floats): argmax,
+// max / exp-sum of z/T (T > 0), and with `draw` the Gumbel-max terms of the
+// draw with counter (element / 4, r, round[r], slot).
+template <int NV>
+__global__ __launch_bounds__(VP_THR) void k_vpart(const float* __restrict__ z0, int64_t row_stride, int V, float T,
+                                                  int vec, int draw, uint64_t seed, const int* __restrict__ round,
+                                                  int slot, VPart* __restrict__ out) {
+  __shared__ float redv[16];
+  __shared__ int redi[16];
+  const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  const float* z = z0 + (int64_t)r * row_stride;
+  float v[NV][4];
+  int e0[NV];
+  float bz = -INFINITY;
+  int bzi = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    e0[j] = (c * NV + j) * VP_CHUNK + tid * 4;
+    load4(z, e0[j], V, vec != 0, v[j]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (e0[j] + w < V) argmax_merge(bz, bzi, v[j][w], e0[j] + w);
+  }
+  vp_argmax(bz, bzi, redv, redi);
+  VPart p;
+  p.zmax = bz;
+  p.zarg = bzi;
+  p.m = 0.f;
+  p.s = 1.f;
+  p.a = -INFINITY;
+  p.ai = 0x7fffffff;
+  p.g = -INFINITY;
+  p.gi = 0x7fffffff;
+  if (T > 0.f) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        v[j][w] = v[j][w] / T;
+        if (e0[j] + w < V) m = fmaxf(m, v[j][w]);
+      }
+    m = block_max(m, redv);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        if (e0[j] + w < V) sum += expf(v[j][w] - m);
+    sum = block_sum(sum, redv);
+    p.m = m;
+    p.s = sum;
+    if (draw) {
+      const int rnd = round[r];
+      float ba = -INFINITY, bg = -INFINITY;
+      int bai = 0x7fffffff, bgi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        if (e0[j] >= V) continue;
+        const u32x4 rr = philox4x32_10(u32x4{(uint32_t)(e0[j] >> 2), (uint32_t)r, (uint32_t)rnd, (uint32_t)slot},
+                                       (uint32_t)seed, (uint32_t)(seed >> 32));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int i = e0[j] + w;
+          if (i >= V) break;
+          const float G = gumbel_of(pick(rr, w));
+          argmax_merge(ba, bai, (v[j][w] - m) + G, i);
+          argmax_merge(bg, bgi, G, i);
+        }
+      }
+      vp_argmax(ba, bai, redv, redi);
+      vp_argmax(bg, bgi, redv, redi);
+      p.a = ba;
+      p.ai = bai;
+      p.g = bg;
+      p.gi = bgi;
+    }
+  }
+  if (tid == 0) out[(int64_t)r * gridDim.x + c] = p;
+}
+
+static int vp_nv(int rows, int V) {
+  int nv = 1;
+  while (nv < 8 && (int64_t)rows * ((V + VP_CHUNK * nv - 1) / (VP_CHUNK * nv)) > VP_MAXWG) nv *= 2;
+  return nv;
+}
+static int vp_nch(int V, int nv) { return (V + VP_CHUNK * nv - 1) / (VP_CHUNK * nv); }
+
+static int launch_vpart(const float* z0, int64_t row_stride, int rows, int V, float T, bool draw, uint64_t seed,
+                        const int* round, int slot, VPart* out, int* nch_out, hipStream_t s) {
+  const int nv = vp_nv(rows, V), nch = vp_nch(V, nv);
+  const int vec = (V % 4 == 0) && (row_stride % 4 == 0) && ((uintptr_t)z0 % 16 == 0);
+  const dim3 grid(nch, rows);
+  switch (nv) {
+    case 1: hipLaunchKernelGGL(k_vpart<1>, grid, dim3(VP_THR), 0, s, z0, row_stride, V, T, vec, (int)draw, seed, round, slot, out); break;
+    case 2: hipLaunchKernelGGL(k_vpart<2>, grid, dim3(VP_THR), 0, s, z0, row_stride, V, T, vec, (int)draw, seed, round, slot, out); break;
+    case 4: hipLaunchKernelGGL(k_vpart<4>, grid, dim3(VP_THR), 0, s, z0, row_stride, V, T, vec, (int)draw, seed, round, slot, out); break;
+    default: hipLaunchKernelGGL(k_vpart<8>, grid, dim3(VP_THR), 0, s, z0, row_stride, V, T, vec, (int)draw, seed, round, slot, out); break;
+  }
+  FC_LAUNCH_CHECK();
+  *nch_out = nch;
+  return FC_OK;
+}
+
+// One wave merges the nch partials of a row: statistics and (with `draw`)
+// the winner of the row's draw.
+struct RowMerge { float M, S; int argmax, tok; };
+__device__ RowMerge wave_merge_row(const VPart* __restrict__ p, int nch, bool samp, bool draw) {
+  const int lane = threadIdx.x & 63;
+  float M = -INFINITY, zm = -INFINITY;
+  int zi = 0x7fffffff;
+  for (int c = lane; c < nch; c += 64) {
+    M = fmaxf(M, p[c].m);
+    argmax_merge(zm, zi, p[c].zmax, p[c].zarg);
+  }
+  M = wave_max(M);
+  wave_argmax(zm, zi);
+  RowMerge rm;
+  rm.argmax = zi;
+  rm.M = 0.f;
+  rm.S = 1.f;
+  rm.tok = zi;
+  if (!samp) return rm;
+  float S = 0.f;
+  for (int c = lane; c < nch; c += 64) S += p[c].s * expf(p[c].m - M);
+  S = wave_sum(S);
+  rm.M = M;
+  rm.S = S;
+  if (draw) {
+    const float lS = logf(S), lf = log_floor();
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int c = lane; c < nch; c += 64) {
+      argmax_merge(bv, bi, p[c].a - ((M - p[c].m) + lS), p[c].ai);
+      argmax_merge(bv, bi, lf + p[c].g, p[c].gi);
+    }
+    wave_argmax(bv, bi);
+    rm.tok = bi;
+  }
+  return rm;
+}
+
+__device__ __forceinline__ fc_rowstat make_rowstat(const RowMerge& rm, int V) {
+  fc_rowstat rs{};
+  rs.mx = rm.M;
+  rs.sum = rm.S;
+  rs.tau = -INFINITY;
+  rs.tie_idx = V;
+  rs.argmax = rm.argmax;
+  return rs;
+}
+
+// Draft step i without top-k: merge of the step's partials (one wave per row),
+// proposal d_{i+1} written where the next chunks read it.
+__global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, int Wv, const VPart* __restrict__ part,
+                                                         int nch) {
+  const int b = blockIdx.x * (VP_THR / 64) + (threadIdx.x >> 6);
+  if (b >= s.B) return;
+  const bool samp = s.T > 0.f;
+  const RowMerge rm = wave_merge_row(part + (int64_t)b * nch, nch, samp, samp);
+  if ((threadIdx.x & 63) == 0) {
+    s.q_stats[b * s.k + i] = make_rowstat(rm, s.V);
+    const int tok = rm.tok;
+    s.drafts[b * s.k + i] = tok;
+    s.tok_v[b * Wv + (Wv - s.k) + i] = tok;
+    if (i + 1 < s.k) s.tok_ds[(i + 1) * s.B + b] = tok;
+  }
+}
+
+// Verify rows without top-k: merge the k+1 rows' partials into p_stats,
+// decide, and record the draw requests for k_draw_part.
+__global__ __launch_bounds__(VP_THR) void k_accept_decide(SpecDev s, const VPart* __restrict__ part, int nch,
+                                                          Decision* __restrict__ ctl) {
+  __shared__ fc_rowstat ps[FC_PMAX + 1];
+  __shared__ Decision d;
+  const int b = blockIdx.x, w = threadIdx.x >> 6;
+  const int R = s.k + 1;
+  const bool samp = s.T > 0.f;
+  for (int j = w; j < R; j += VP_THR / 64) {
+    const RowMerge rm = wave_merge_row(part + ((int64_t)b * R + j) * nch, nch, samp, false);
+    if ((threadIdx.x & 63) == 0) {
+      const fc_rowstat rs = make_rowstat(rm, s.V);
+      ps[j] = rs;
+      s.p_stats[b * R + j] = rs;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  decide(s, b, ps, d);
+  ctl[b] = d;
+}
+
+// Chunk partials of the rejection draw (z = 0, slot 48, from p or from the
+// residual max(0, p - q)) and the bonus draw (z = 1, slot 49, from p) of
+// each row, as requested by k_accept_decide.
+template <int NV>
+__global__ __launch_bounds__(VP_THR) void k_draw_part(SpecDev s, const Decision* __restrict__ ctl, int vec,
+                                                      DPart* __restrict__ out) {
+  __shared__ float redv[16];
+  __shared__ int redi[16];
+  const int c = blockIdx.x, b = blockIdx.y, q = blockIdx.z, tid = threadIdx.x;
+  const Decision& d = ctl[b];
+  int mode, row, slot;
+  if (q == 0) {
+    mode = d.mode > 0 ? d.mode : 0;
+    row = d.row;
+    slot = SLOT_REJECT;
+  } else {
+    mode = d.bonus_draw ? 1 : 0;
+    row = d.kp;
+    slot = SLOT_BONUS;
+  }
+  if (mode == 0) return;  // uniform over the block
+  const int K = s.k, V = s.V;
+  const float T = s.T;
+  const float* zp = s.p_logits + ((int64_t)b * (K + 1) + row) * V;
+  const fc_rowstat ps = s.p_stats[b * (K + 1) + row];
+  const float* zq = s.q_logits + ((int64_t)b * K + min(row, K - 1)) * V;
+  const fc_rowstat qs = s.q_stats[b * K + min(row, K - 1)];
+  const int rnd = s.round[b];
+  float bs = -INFINITY, bA = -INFINITY, bg = -INFINITY, R = 0.f;
+  int bsi = 0x7fffffff, bAi = 0x7fffffff, bgi = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = (c * NV + j) * VP_CHUNK + tid * 4;
+    if (e >= V) continue;
+    float vp[4], vq[4];
+    load4(zp, e, V, vec != 0, vp);
+    if (mode == 2) load4(zq, e, V, vec != 0, vq);
+    const u32x4 rr = philox4x32_10(u32x4{(uint32_t)(e >> 2), (uint32_t)b, (uint32_t)rnd, (uint32_t)slot},
+                                   (uint32_t)s.seed, (uint32_t)(s.seed >> 32));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int i = e + w;
+      if (i >= V) break;
+      const float G = gumbel_of(pick(rr, w));
+      const float p = expf(vp[w] / T - ps.mx) / ps.sum;
+      argmax_merge(bs, bsi, logf(fmaxf(p, 1e-10f)) + G, i);
+      if (mode == 2) {
+        const float rv = fmaxf(p - expf(vq[w] / T - qs.mx) / qs.sum, 0.f);
+        R += rv;
+        if (rv > 0.f) argmax_merge(bA, bAi, logf(rv) + G, i);
+        argmax_merge(bg, bgi, G, i);
+      }
+    }
+  }
+  vp_argmax(bs, bsi, redv, redi);
+  DPart o;
+  o.sc = bs;
+  o.si = bsi;
+  o.A = -INFINITY;
+  o.Ai = 0x7fffffff;
+  o.g = -INFINITY;
+  o.gi = 0x7fffffff;
+  o.R = 0.f;
+  o.pad = 0;
+  if (mode == 2) {
+    vp_argmax(bA, bAi, redv, redi);
+    vp_argmax(bg, bgi, redv, redi);
+    R = block_sum(R, redv);
+    o.A = bA;
+    o.Ai = bAi;
+    o.g = bg;
+    o.gi = bgi;
+    o.R = R;
+  }
+  if (tid == 0) out[((int64_t)b * 2 + q) * gridDim.x + c] = o;
+}
+
+// Winner of one draw from its chunk partials (one wave): the residual
+// max(0, p - q) renormalised when its mass is positive, else p.
+__device__ int wave_merge_draw(const DPart* __restrict__ p, int nch, bool residual) {
+  const int lane = threadIdx.x & 63;
+  float R = 0.f;
+  if (residual) {
+    for (int c = lane; c < nch; c += 64) R += p[c].R;
+    R = wave_sum(R);
+  }
+  const bool use_r = residual && R > 0.f;
+  const float lR = use_r ? logf(R) : 0.f, lf = log_floor();
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int c = lane; c < nch; c += 64) {
+    if (use_r) {
+      argmax_merge(bv, bi, p[c].A - lR, p[c].Ai);
+      argmax_merge(bv, bi, lf + p[c].g, p[c].gi);
+    } else {
+      argmax_merge(bv, bi, p[c].sc, p[c].si);
+    }
+  }
+  wave_argmax(bv, bi);
+  return bi;
+}
+
+// Rejection / bonus tokens from the draw partials, then the bookkeeping.
+__global__ __launch_bounds__(64) void k_accept_finish(SpecDev s, const Decision* __restrict__ ctl,
+                                                      const DPart* __restrict__ part, int nch) {
+  __shared__ int em[32];
+  const int b = blockIdx.x;
+  const Decision* d = ctl + b;
+  const int mode = d->mode, bonus_draw = d->bonus_draw;
+  if (mode < 0) {
+    if (threadIdx.x == 0) finished_row(s, b);
+    return;
+  }
+  int trej = -1, tbonus = -1;
+  if (mode > 0) trej = wave_merge_draw(part + (int64_t)b * 2 * nch, nch, mode == 2);
+  if (bonus_draw) tbonus = wave_merge_draw(part + ((int64_t)b * 2 + 1) * nch, nch, false);
+  if (threadIdx.x != 0) return;
+  int n = d->n;
+  for (int i = 0; i < n; ++i) em[i] = d->emitted[i];
+  if (mode > 0) em[n++] = trej;
+  if (bonus_draw) em[n++] = tbonus;
+  bookkeep(s, b, em, n, d->acc, d->rej, d->bonus, d->kp, s.round[b]);
+}
+
+// Layout of fc_spec_state.part: Decision[B] | VPart[B*(k+1)][nch1] | DPart[B][2][nch1],
+// nch1 = chunks per row at NV = 1 (the most any pass uses).
+struct PartLayout {
+  Decision* ctl;
+  VPart* vp;
+  DPart* dp;
+  int64_t bytes;
+};
+static PartLayout part_layout(void* base, int B, int K, int V) {
+  const int64_t nch1 = vp_nch(V, 1);
+  PartLayout L;
+  const int64_t o_vp = fc_align((int64_t)B * sizeof(Decision));
+  const int64_t o_dp = o_vp + fc_align((int64_t)B * (K + 1) * nch1 * sizeof(VPart));
+  L.bytes = o_dp + fc_align((int64_t)B * 2 * nch1 * sizeof(DPart));
+  char* p = (char*)base;
+  L.ctl = (Decision*)p;
+  L.vp = (VPart*)(p + o_vp);
+  L.dp = (DPart*)(p + o_dp);
+  return L;
+}
+
+extern "C" int64_t fc_spec_part_bytes(int32_t batch, int32_t k, int32_t vocab) {
+  if (batch <= 0 || k <= 0 || vocab <= 0) return -1;
+  return part_layout(nullptr, batch, k, vocab).bytes;
+}
+
+// The chunked passes serve rows without a top-k filter (and greedy rows: the
+// top-k set does not move the argmax); the filtered case keeps one
+// workgroup per row for its radix select.
+static bool chunked(const fc_spec_state* st) {
+  return !(st->temperature > 0.f) || st->top_k <= 0 || st->top_k >= st->vocab;
+}
+
 static int check_spec(const fc_spec_state* st) {
   FC_CHECK_ARG(st && st->batch > 0 && st->k > 0 && st->k <= 16 && st->vocab > 0, "spec state sizes (k in 1..16)");
   FC_CHECK_ARG(st->t_len && st->d_len && st->gen && st->gen_n && st->result && st->q_logits && st->p_logits &&
-                   st->q_stats && st->p_stats && st->drafts && st->tok_v && st->tok_ds && st->tok_d0,
+                   st->q_stats && st->p_stats && st->drafts && st->tok_v && st->tok_ds && st->tok_d0 && st->part,
                "spec state pointers");
+  FC_CHECK_ARG(st->part_bytes >= fc_spec_part_bytes(st->batch, st->k, st->vocab),
+               "part_bytes below fc_spec_part_bytes(batch, k, vocab)");
   return FC_OK;
 }
 
@@ -490,10 +918,31 @@ extern "C" int32_t fc_spec_accept(const fc_spec_state* st, int32_t w_verify, voi
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
   SpecDev d = to_dev(st);
-  rc = fc_launch_row_stats(st->p_logits, st->batch * (st->k + 1), st->vocab, st->temperature, st->top_k,
-                           st->p_stats, s);
+  const int B = st->batch, K = st->k, V = st->vocab;
+  if (!chunked(st)) {
+    rc = fc_launch_row_stats(st->p_logits, B * (K + 1), V, st->temperature, st->top_k, st->p_stats, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_accept, dim3(B), dim3(NTHR), 0, s, d);
+    FC_LAUNCH_CHECK();
+    return FC_OK;
+  }
+  const PartLayout L = part_layout(st->part, B, K, V);
+  int nch = 0;
+  rc = launch_vpart(st->p_logits, V, B * (K + 1), V, st->temperature, false, st->seed, st->round, 0, L.vp, &nch, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_accept, dim3(st->batch), dim3(NTHR), 0, s, d);
+  hipLaunchKernelGGL(k_accept_decide, dim3(B), dim3(VP_THR), 0, s, d, L.vp, nch, L.ctl);
+  FC_LAUNCH_CHECK();
+  const int nv = vp_nv(B, V), dch = vp_nch(V, nv);
+  const int vec = (V % 4 == 0) && ((uintptr_t)st->p_logits % 16 == 0) && ((uintptr_t)st->q_logits % 16 == 0);
+  const dim3 grid(dch, B, 2);
+  switch (nv) {
+    case 1: hipLaunchKernelGGL(k_draw_part<1>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
+    case 2: hipLaunchKernelGGL(k_draw_part<2>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
+    case 4: hipLaunchKernelGGL(k_draw_part<4>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
+    default: hipLaunchKernelGGL(k_draw_part<8>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
+  }
+  FC_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_accept_finish, dim3(B), dim3(64), 0, s, d, L.ctl, L.dp, dch);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
@@ -513,6 +962,8 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
   FC_CHECK_ARG(w_verify >= K + 1 && w_verify <= FC_PMAX + K, "w_verify must be in [k+1, FC_PMAX+k]");
   hipLaunchKernelGGL(k_spec_plan, dim3((B + 255) / 256), dim3(256), 0, s, d, w_draft, w_verify);
   FC_LAUNCH_CHECK();
+  const bool fast = chunked(st);
+  const PartLayout L = part_layout(st->part, B, K, V);
   for (int i = 0; i < K; ++i) {
     fc_chunk ch{};
     if (i == 0) {
@@ -531,7 +982,15 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
     ch.logits_stride = (int64_t)K * V;
     rc = fc_forward(draft, dcache, &ch, work, work_bytes, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i, w_verify);
+    if (fast) {
+      int nch = 0;
+      rc = launch_vpart(st->q_logits + (int64_t)i * V, (int64_t)K * V, B, V, st->temperature, st->temperature > 0.f,
+                        st->seed, st->round, i, L.vp, &nch, s);
+      if (rc) return rc;
+      hipLaunchKernelGGL(k_draft_finish, dim3((B + 3) / 4), dim3(VP_THR), 0, s, d, i, w_verify, L.vp, nch);
+    } else {
+      hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i, w_verify);
+    }
     FC_LAUNCH_CHECK();
   }
   fc_chunk vch{};

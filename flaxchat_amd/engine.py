@@ -145,9 +145,11 @@ class SpecSession:
                 q_logits=torch.zeros(B, k, V, dtype=torch.float32, device=dev),
                 p_logits=torch.zeros(B, k + 1, V, dtype=torch.float32, device=dev),
                 q_stats=torch.zeros(B * k * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev),
-                p_stats=torch.zeros(B * (k + 1) * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev))
+                p_stats=torch.zeros(B * (k + 1) * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev),
+                part=torch.zeros(lib().fc_spec_part_bytes(B, k, V), dtype=torch.uint8, device=dev))
         self.state = FcSpecState(B, k, self.max_tokens, self.gen_cap, V, self.temperature, self.top_k, self.seed,
-                                 *[self.bufs[n].data_ptr() for n in _lib._SPEC_PTRS])
+                                 *[self.bufs[n].data_ptr() for n in _lib._SPEC_PTRS],
+                                 self.bufs["part"].data_ptr(), self.bufs["part"].numel())
         self.ws = Workspace(dev)          # captured by the round graphs: never reallocated after capture
         self.ws_catchup = Workspace(dev)  # prefill / catch-up
         nb = max(lib().fc_forward_workspace_bytes(ctypes.byref(m.desc), B, w, w)

@@ -127,6 +127,8 @@ typedef struct fc_spec_state {
   float* p_logits;   /* [B][k+1][V]                                            */
   fc_rowstat* q_stats; /* [B][k]                                               */
   fc_rowstat* p_stats; /* [B][k+1]                                             */
+  void* part;          /* vocab-pass partials, fc_spec_part_bytes(batch, k, vocab) */
+  int64_t part_bytes;
 } fc_spec_state;
 
 #define FC_RES_STRIDE 40
@@ -186,6 +188,10 @@ int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
                       void* work, int64_t work_bytes, void* stream);
 /* w_draft >= every active row's draft pending count (chunk width of draft
  * step 0); w_verify >= every active row's target pending count + k. */
+
+/* Bytes of fc_spec_state.part: per-chunk partials of the vocab-wide passes
+ * (row statistics and Gumbel-max draws split over many workgroups). */
+int64_t fc_spec_part_bytes(int32_t batch, int32_t k, int32_t vocab);
 
 /* Accept/reject step alone on given logits (flaxchat/engine.py:525-592);
  * updates the state like fc_spec_round does. */
