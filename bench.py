@@ -57,7 +57,8 @@ ATTN_TRAFFIC_RATIO = 1.14
 
 
 def attention_roofline(sess, n_iter=20):
-    """Time the verify attention at the session's current lengths."""
+    """Time the verify attention at the session's current lengths: every row
+    feeds k+1 queries (one pending token and k drafts) at its cache length."""
     import torch
     from flaxchat_amd import _lib
     T = sess.T
@@ -66,10 +67,10 @@ def attention_roofline(sess, n_iter=20):
     dev = T.device
     s = sess.stream
     t_len = sess.bufs["t_len"].cpu().numpy().astype(np.int64)
-    q = torch.randn(B, W, T.H, T.hd, device=dev).to(torch.bfloat16)
+    q = torch.randn(B * W, T.H, T.hd, device=dev).to(torch.bfloat16)
     y = torch.empty_like(q)
     start = sess.bufs["t_len"].clone()
-    nvalid = torch.full((B,), W, dtype=torch.int32, device=dev)
+    row_off = torch.arange(0, B * W + 1, W, dtype=torch.int32, device=dev)
     cap = sess.tcache.cap
     res = {}
     es = 2
@@ -83,7 +84,7 @@ def attention_roofline(sess, n_iter=20):
         vp = sess.tcache.v.data_ptr() + layer * layer_elems * es
         def launch():
             _lib.check(_lib.lib().fc_attention(q.data_ptr(), kp, vp, y.data_ptr(), B, W, T.H, T.G, T.hd, cap,
-                                               start.data_ptr(), nvalid.data_ptr(), win, max_keys, 1,
+                                               row_off.data_ptr(), start.data_ptr(), win, max_keys, 1,
                                                ws.data_ptr(), ws.numel(), s.cuda_stream), "attention")
         with torch.cuda.stream(s):
             for _ in range(3):

@@ -40,7 +40,8 @@ class FcCache(Structure):
 
 
 class FcChunk(Structure):
-    _fields_ = [("W", c_int32), ("tokens", c_void_p), ("start", c_void_p), ("nvalid", c_void_p),
+    _fields_ = [("max_tokens", c_int32), ("max_per_row", c_int32), ("typ_tokens", c_int32),
+                ("tokens", c_void_p), ("row_off", c_void_p), ("start", c_void_p),
                 ("n_out", c_int32), ("logits", c_void_p), ("logits_stride", c_int64)]
 
 
@@ -50,8 +51,8 @@ class FcRowstat(Structure):
 
 
 _SPEC_PTRS = ["t_len", "d_len", "t_pend", "d_pend", "t_pend_n", "d_pend_n", "t_dirty", "d_dirty",
-              "gen", "gen_n", "prompt_len", "round", "result",
-              "tok_d0", "n_d0", "start_d", "tok_ds", "ones", "tok_v", "start_v", "n_v", "drafts",
+              "gen", "gen_n", "prompt_len", "round", "stall", "result",
+              "tok_d0", "off_d0", "start_d", "tok_ds", "off_ds", "tok_v", "off_v", "start_v", "drafts",
               "q_logits", "p_logits", "q_stats", "p_stats"]
 
 
@@ -61,10 +62,10 @@ class FcSpecState(Structure):
                 + [(n, c_void_p) for n in _SPEC_PTRS] + [("part", c_void_p), ("part_bytes", c_int64)])
 
 
-EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forward", "fc_gemm",
-           "fc_attention_workspace_bytes", "fc_attention", "fc_row_stats", "fc_spec_round",
-           "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_graph_begin", "fc_graph_end",
-           "fc_graph_launch", "fc_graph_destroy"]
+EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forward", "fc_gemm", "fc_pack_operand",
+           "fc_attention_workspace_bytes", "fc_attention", "fc_row_stats", "fc_spec_workspace_bytes",
+           "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_graph_begin",
+           "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
 
 _lib = None
 
@@ -73,22 +74,26 @@ def _declare(L):
     vp, i32, i64, f32 = c_void_p, c_int32, c_int64, c_float
     L.fc_last_error.restype = c_char_p
     L.fc_version.restype = i32
-    L.fc_forward_workspace_bytes.argtypes = [POINTER(FcModel), i32, i32, i32]
+    L.fc_forward_workspace_bytes.argtypes = [POINTER(FcModel), i32, i32, i32, i32]
     L.fc_forward_workspace_bytes.restype = i64
     L.fc_forward.argtypes = [POINTER(FcModel), POINTER(FcCache), POINTER(FcChunk), vp, i64, vp]
     L.fc_forward.restype = i32
     L.fc_gemm.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp]
     L.fc_gemm.restype = i32
+    L.fc_pack_operand.argtypes = [vp, vp, i32, i32, vp]
+    L.fc_pack_operand.restype = i32
     L.fc_attention_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.fc_attention_workspace_bytes.restype = i64
     L.fc_attention.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64, vp]
+    L.fc_spec_workspace_bytes.argtypes = [POINTER(FcModel), POINTER(FcModel), i32, i32]
+    L.fc_spec_workspace_bytes.restype = i64
     L.fc_attention.restype = i32
     L.fc_row_stats.argtypes = [vp, i32, i32, f32, i32, vp, vp]
     L.fc_row_stats.restype = i32
     L.fc_spec_round.argtypes = [POINTER(FcModel), POINTER(FcCache), POINTER(FcModel), POINTER(FcCache),
-                                POINTER(FcSpecState), i32, i32, vp, i64, vp]
+                                POINTER(FcSpecState), vp, i64, vp]
     L.fc_spec_round.restype = i32
-    L.fc_spec_accept.argtypes = [POINTER(FcSpecState), i32, vp]
+    L.fc_spec_accept.argtypes = [POINTER(FcSpecState), vp]
     L.fc_spec_accept.restype = i32
     L.fc_spec_part_bytes.argtypes = [i32, i32, i32]
     L.fc_spec_part_bytes.restype = i64

@@ -11,9 +11,9 @@
 // exact zeros in fp32, so reading only the visible keys is the same sum.
 //
 // bf16 path (head_dim 128): one workgroup per (row, KV group, query block of
-// 16 columns, key split). Columns are (slot, head-in-group) pairs, so a
-// verify chunk's k+1 tokens and the GQA heads of a group share every K/V
-// tile read. Each wave walks 32-key tiles with two matrix-core products:
+// 16 columns, key split). Columns are (token, head-in-group) pairs of the
+// row's packed tokens, so a verify chunk's tokens and the GQA heads of a
+// group share every K/V tile read. Each wave walks 32-key tiles with two matrix-core products:
 //   S^T = K Q^T   (16 keys x 16 columns per MFMA; two MFMAs per tile, with
 //                  the key rows interleaved so each lane ends up holding 8
 //                  consecutive keys of its column), then online softmax in
@@ -28,25 +28,24 @@
 #include "fc_internal.h"
 
 // ---------------------------------------------------------------------------
-// Prologue: one wave per (token row m, head slot hh in [0, H + 2G)).
+// Prologue: one wave per (packed token m, head slot hh in [0, H + 2G)).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv, const T* __restrict__ h,
                                                   const int* __restrict__ tokens, const float* __restrict__ rcos,
                                                   const float* __restrict__ rsin, int rope_len,
                                                   const T* __restrict__ ve, const float* __restrict__ ve_gate,
-                                                  int D, T* __restrict__ kc, T* __restrict__ vc, int B, int W, int H,
-                                                  int G, int hd, int cap, const int* __restrict__ start,
-                                                  const int* __restrict__ nvalid, T* __restrict__ q) {
+                                                  int D, T* __restrict__ kc, T* __restrict__ vc, int Mcap,
+                                                  const int* __restrict__ Mdev, int H, int G, int hd, int cap,
+                                                  const int* __restrict__ tok_row, const int* __restrict__ tok_pos,
+                                                  T* __restrict__ q) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int NH = H + 2 * G;
   const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  if (item >= (int64_t)B * W * NH) return;
+  if (item >= (int64_t)Mcap * NH) return;
   const int m = (int)(item / NH), hh = (int)(item % NH);
-  const int b = m / W, slot = m - b * W;
-  const int n = nvalid[b];
-  const bool valid = slot >= W - n;
-  const int pos = start[b] + slot - (W - n);
+  if (m >= *Mdev) return;
+  const int b = tok_row[m], pos = tok_pos[m];
   const int half = hd >> 1;
   const bool act = lane < half;
   const float* row = qkv + ((int64_t)m * NH + hh) * hd;
@@ -64,10 +63,10 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
     if (hh < H) {
       if (act) {
         T* qo = q + ((int64_t)m * H + hh) * hd;
-        st<T>(qo, lane, valid ? y1 : 0.f);
-        st<T>(qo, lane + half, valid ? y2 : 0.f);
+        st<T>(qo, lane, y1);
+        st<T>(qo, lane + half, y2);
       }
-    } else if (valid && act && pos < cap) {
+    } else if (act && pos < cap) {
       const int g = hh - H;
       T* ko = kc + (((int64_t)b * G + g) * cap + pos) * hd;
       st<T>(ko, lane, y1);
@@ -76,7 +75,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
   } else {
     const int g = hh - H - G;
     if (ve != nullptr) {
-      float part = lane < 12 ? ld<T>(h, (int64_t)m * D + lane) * ve_gate[g * 12 + lane] : 0.f;
+      float part = lane < 12 ? ld<T>(h, act_idx<T>(m, lane, D)) * ve_gate[g * 12 + lane] : 0.f;
       const float z = wave_sum(part);
       const float gate = 3.f * (1.f / (1.f + expf(-z)));
       const int tok = tokens[m];
@@ -86,7 +85,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
         x2 = x2 + gate * ld<T>(vr, lane + half);
       }
     }
-    if (valid && act && pos < cap) {
+    if (act && pos < cap) {
       T* vb = vc + ((((int64_t)b * G + g) * (cap / 32) + pos / 32) * hd) * 32;
       st<T>(vb, (int64_t)lane * 32 + (pos & 31), x1);
       st<T>(vb, (int64_t)(lane + half) * 32 + (pos & 31), x2);
@@ -95,26 +94,26 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
 }
 
 int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const fc_model* m, int layer,
-                       const fc_cache* c, const int* start, const int* nvalid, int B, int W, void* q,
+                       const fc_cache* c, const int* tok_row, const int* tok_pos, int Mcap, const int* Mdev, void* q,
                        hipStream_t s) {
   const fc_layer& L = m->layers[layer];
   const int H = m->n_head, G = m->n_kv_head, hd = m->head_dim;
   FC_CHECK_ARG(hd <= 128 && hd % 2 == 0, "head_dim must be even and <= 128");
   const int64_t layer_elems = (int64_t)c->batch * G * c->cap * hd;
-  const int64_t items = (int64_t)B * W * (H + 2 * G);
+  const int64_t items = (int64_t)Mcap * (H + 2 * G);
   const dim3 grid((unsigned)((items + 3) / 4));
   if (m->dtype == FC_BF16) {
     bf16_t* kc = (bf16_t*)c->k + layer_elems * layer;
     bf16_t* vc = (bf16_t*)c->v + layer_elems * layer;
     hipLaunchKernelGGL(k_prologue<bf16_t>, grid, dim3(256), 0, s, qkv, (const bf16_t*)h, tokens, m->rope_cos,
-                       m->rope_sin, m->rope_len, (const bf16_t*)L.ve, L.ve_gate, m->n_embd, kc, vc, B, W, H, G, hd,
-                       c->cap, start, nvalid, (bf16_t*)q);
+                       m->rope_sin, m->rope_len, (const bf16_t*)L.ve, L.ve_gate, m->n_embd, kc, vc, Mcap, Mdev, H, G,
+                       hd, c->cap, tok_row, tok_pos, (bf16_t*)q);
   } else {
     float* kc = (float*)c->k + layer_elems * layer;
     float* vc = (float*)c->v + layer_elems * layer;
     hipLaunchKernelGGL(k_prologue<float>, grid, dim3(256), 0, s, qkv, (const float*)h, tokens, m->rope_cos,
-                       m->rope_sin, m->rope_len, (const float*)L.ve, L.ve_gate, m->n_embd, kc, vc, B, W, H, G, hd,
-                       c->cap, start, nvalid, (float*)q);
+                       m->rope_sin, m->rope_len, (const float*)L.ve, L.ve_gate, m->n_embd, kc, vc, Mcap, Mdev, H, G,
+                       hd, c->cap, tok_row, tok_pos, (float*)q);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
@@ -133,24 +132,25 @@ __device__ __forceinline__ uint32_t pack2bf(float lo, float hi) {
 
 __global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
                                                    const bf16_t* __restrict__ vc, float* __restrict__ part_o,
-                                                   float* __restrict__ part_ml, int W, int H, int G, int cap,
-                                                   const int* __restrict__ start, const int* __restrict__ nvalid,
+                                                   float* __restrict__ part_ml, int H, int G, int cap,
+                                                   const int* __restrict__ row_off, const int* __restrict__ start,
                                                    int window, int split_keys, int nsplit, int nqblk,
                                                    float scale_log2) {
   constexpr int HD = 128;
   const int split = blockIdx.x, qb = blockIdx.y, bg = blockIdx.z;
   const int b = bg / G, g = bg - b * G, rep = H / G;
-  const int n = nvalid[b], s0 = start[b], off = W - n;
+  const int base = row_off[b], n = row_off[b + 1] - base, s0 = start[b];
+  const int ncol = n * rep;
+  if (qb * 16 >= ncol) return;  // no query of this row in the block: combine reads nothing here
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, g4 = lane >> 4;
-  const int ncol = W * rep;
   const int64_t pidx = ((int64_t)bg * nqblk + qb) * nsplit + split;
 
   // key range of the whole query block
-  const int f = max(qb * 16, off * rep), lcol = min(qb * 16 + 15, ncol - 1);
+  const int f = qb * 16, lcol = min(qb * 16 + 15, ncol - 1);
   int kbeg = 0, kend = 0;
-  if (f <= lcol) {
-    const int pf = s0 + f / rep - off, pl = s0 + lcol / rep - off;
+  {
+    const int pf = s0 + f / rep, pl = s0 + lcol / rep;
     const int klo = window > 0 ? max(0, pf - window) : 0;
     const int khi = min(pl + 1, cap);
     kbeg = klo + split * split_keys;
@@ -166,14 +166,14 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q,
   // this lane's query column
   const int col = qb * 16 + c;
   const int j = col / rep, head = g * rep + (col - j * rep);
-  const bool cvalid = col < ncol && j >= off;
-  const int pos_c = s0 + j - off;
+  const bool cvalid = col < ncol;
+  const int pos_c = s0 + j;
   const int lo_c = window > 0 ? max(0, pos_c - window) : 0;
 
   const uint4 zero = {0u, 0u, 0u, 0u};
   uint4 qf[4];
   {
-    const bf16_t* qr = q + (((int64_t)b * W + (cvalid ? j : 0)) * H + head) * HD + 8 * g4;
+    const bf16_t* qr = q + ((int64_t)(base + (cvalid ? j : 0)) * H + head) * HD + 8 * g4;
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = cvalid ? *(const uint4*)(qr + 32 * s) : zero;
   }
@@ -284,44 +284,53 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q,
   }
 }
 
-// one wave per (token row, head): merge the key splits and normalise
+// One workgroup per (row, KV group, query block): merge the key splits of
+// its 16 columns and normalise; thread t owns column t / 16 and 8
+// consecutive dimensions.
 template <typename T>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
-                                                      const float* __restrict__ part_ml, T* __restrict__ y, int B,
-                                                      int W, int H, int G, int nqblk, int nsplit,
-                                                      const int* __restrict__ nvalid) {
+                                                      const float* __restrict__ part_ml, T* __restrict__ y, int H,
+                                                      int G, int nqblk, int nsplit, const int* __restrict__ row_off) {
   constexpr int HD = 128;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  if (item >= (int64_t)B * W * H) return;
-  const int m = (int)(item / H), h = (int)(item % H);
-  const int b = m / W, j = m - b * W;
-  const int rep = H / G, g = h / rep;
-  T* yo = y + ((int64_t)m * H + h) * HD;
-  if (j < W - nvalid[b]) {
-    st<T>(yo, lane, 0.f);
-    st<T>(yo, lane + 64, 0.f);
-    return;
-  }
-  const int col = j * rep + (h - g * rep), qb = col >> 4, c = col & 15;
-  const int64_t base = ((int64_t)(b * G + g) * nqblk + qb) * nsplit;
+  const int qb = blockIdx.x, bg = blockIdx.y;
+  const int b = bg / G, g = bg - b * G, rep = H / G;
+  const int base = row_off[b], ncol = (row_off[b + 1] - base) * rep;
+  const int c = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+  const int col = qb * 16 + c;
+  if (col >= ncol) return;
+  const int j = col / rep, head = g * rep + (col - j * rep);
+  const int64_t pb = ((int64_t)bg * nqblk + qb) * nsplit;
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[((base + s) * 16 + c) * 2]);
-  float o0 = 0.f, o1 = 0.f, L = 0.f;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[((pb + s) * 16 + c) * 2]);
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
   if (M != -INFINITY) {
     for (int s = 0; s < nsplit; ++s) {
-      const float ms = part_ml[((base + s) * 16 + c) * 2];
+      const float ms = part_ml[((pb + s) * 16 + c) * 2];
       if (ms == -INFINITY) continue;
       const float a = exp2f(ms - M);
-      L += a * part_ml[((base + s) * 16 + c) * 2 + 1];
-      const float* po = part_o + ((base + s) * 16 + c) * HD;
-      o0 += a * po[lane];
-      o1 += a * po[lane + 64];
+      L += a * part_ml[((pb + s) * 16 + c) * 2 + 1];
+      const float4* po = (const float4*)(part_o + ((pb + s) * 16 + c) * HD + d0);
+      const float4 u0 = po[0], u1 = po[1];
+      o[0] += a * u0.x; o[1] += a * u0.y; o[2] += a * u0.z; o[3] += a * u0.w;
+      o[4] += a * u1.x; o[5] += a * u1.y; o[6] += a * u1.z; o[7] += a * u1.w;
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  st<T>(yo, lane, o0 * inv);
-  st<T>(yo, lane + 64, o1 * inv);
+  // y is the c_proj GEMM's operand [token][H * 128]: 8 consecutive k are one
+  // contiguous 16-byte group in both layouts
+  T* yo = y + act_idx<T>(base + j, head * HD + d0, H * HD);
+  if constexpr (sizeof(T) == 2) {
+    uint4 pk;
+    pk.x = (uint32_t)f2bf(o[0] * inv) | ((uint32_t)f2bf(o[1] * inv) << 16);
+    pk.y = (uint32_t)f2bf(o[2] * inv) | ((uint32_t)f2bf(o[3] * inv) << 16);
+    pk.z = (uint32_t)f2bf(o[4] * inv) | ((uint32_t)f2bf(o[5] * inv) << 16);
+    pk.w = (uint32_t)f2bf(o[6] * inv) | ((uint32_t)f2bf(o[7] * inv) << 16);
+    *(uint4*)yo = pk;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st<T>(yo, i, o[i] * inv);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -330,22 +339,18 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
 #define VALU_MAXK 8192
 template <typename T>
 __global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, const T* __restrict__ kc,
-                                                   const T* __restrict__ vc, T* __restrict__ y, int W, int H, int G,
-                                                   int hd, int cap, const int* __restrict__ start,
-                                                   const int* __restrict__ nvalid, int window, float scale) {
+                                                   const T* __restrict__ vc, T* __restrict__ y, int H, int G, int hd,
+                                                   int cap, const int* __restrict__ row_off,
+                                                   const int* __restrict__ start, int window, float scale) {
   __shared__ float qs[128];
   __shared__ float sc[VALU_MAXK];
   __shared__ float red[16];
-  const int m = blockIdx.x / H, h = blockIdx.x - (blockIdx.x / H) * H;
-  const int b = m / W, j = m - b * W;
-  const int n = nvalid[b], off = W - n;
+  const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int base = row_off[b];
+  if (j >= row_off[b + 1] - base) return;
+  const int m = base + j;
   const int rep = H / G, g = h / rep;
-  T* yo = y + ((int64_t)m * H + h) * hd;
-  if (j < off) {
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) st<T>(yo, d, 0.f);
-    return;
-  }
-  const int pos = min(start[b] + j - off, cap - 1);
+  const int pos = min(start[b] + j, cap - 1);
   const int lo = window > 0 ? max(0, pos - window) : 0;
   const int nk = min(pos - lo + 1, VALU_MAXK);
   const int64_t bg = (int64_t)b * G + g;
@@ -377,18 +382,21 @@ __global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, cons
       const int key = lo + i;
       acc += sc[i] * ld<T>(vb, ((int64_t)(key >> 5) * hd + d) * 32 + (key & 31));
     }
-    st<T>(yo, d, acc);
+    st<T>(y, act_idx<T>(m, h * hd + d, H * hd), acc);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-AttnGrid fc_attn_grid(int batch, int W, int n_head, int n_kv_head, int max_keys) {
+AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, int n_kv_head, int max_keys) {
   AttnGrid a;
   const int rep = n_head / n_kv_head;
-  a.nqblk = (W * rep + 15) / 16;
-  const int64_t units = (int64_t)batch * n_kv_head * a.nqblk;
+  a.nqblk = (max_per_row * rep + 15) / 16;
+  // split the key range so that the blocks a typical chunk fills reach ~4
+  // workgroups per CU
+  const int typ_blk = std::min(a.nqblk, std::max(1, (typ_per_row * rep + 15) / 16));
+  const int64_t units = (int64_t)batch * n_kv_head * typ_blk;
   const int range = max(max_keys, 1);
   int want = (int)((1024 + units - 1) / units);
   want = max(1, min(want, (range + 127) / 128));
@@ -399,60 +407,64 @@ AttnGrid fc_attn_grid(int batch, int W, int n_head, int n_kv_head, int max_keys)
   return a;
 }
 
-int64_t fc_attn_part_bytes(int batch, int W, int n_head, int n_kv_head, int head_dim, int max_keys) {
+int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head, int head_dim, int max_keys) {
   if (head_dim != 128) return 0;
-  AttnGrid a = fc_attn_grid(batch, W, n_head, n_kv_head, max_keys);
-  const int64_t units = (int64_t)batch * n_kv_head * a.nqblk * a.nsplit * 16;
+  // fc_attn_grid never makes more splits than ceil(1024 / units), and one
+  // token per row gives the fewest units
+  AttnGrid a = fc_attn_grid(batch, max_per_row, 1, n_head, n_kv_head, max_keys);
+  const int64_t units1 = (int64_t)batch * n_kv_head;
+  const int64_t nsplit = std::max<int64_t>(a.nsplit, (1024 + units1 - 1) / units1);
+  const int64_t units = (int64_t)batch * n_kv_head * a.nqblk * nsplit * 16;
   return fc_align(units * 128 * 4) + fc_align(units * 2 * 4);
 }
 
-int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int W, int H, int G, int hd,
-                        int cap, const int* start, const int* nvalid, int window, int max_keys, int dtype,
-                        void* part, int64_t part_bytes, hipStream_t s) {
+int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_per_row,
+                        int typ_per_row, int H, int G, int hd, int cap, const int* row_off, const int* start,
+                        int window, int max_keys, int dtype, void* part, int64_t part_bytes, hipStream_t s) {
   FC_CHECK_ARG(H % G == 0, "n_head must be a multiple of n_kv_head");
   FC_CHECK_ARG(cap % 32 == 0, "cache capacity must be a multiple of 32");
+  FC_CHECK_ARG(max_per_row > 0, "max_per_row");
   const float scale = 1.f / sqrtf((float)hd);
   if (dtype == FC_BF16 && hd == 128) {
-    AttnGrid a = fc_attn_grid(B, W, H, G, max_keys);
+    AttnGrid a = fc_attn_grid(B, max_per_row, typ_per_row, H, G, max_keys);
     const int64_t units = (int64_t)B * G * a.nqblk * a.nsplit * 16;
     FC_CHECK_ARG(part != nullptr && part_bytes >= fc_align(units * 128 * 4) + fc_align(units * 2 * 4),
                  "attention workspace too small");
     float* po = (float*)part;
     float* pml = (float*)((char*)part + fc_align(units * 128 * 4));
     hipLaunchKernelGGL(k_attn_mfma, dim3(a.nsplit, a.nqblk, B * G), dim3(256), 0, s, (const bf16_t*)q,
-                       (const bf16_t*)kc, (const bf16_t*)vc, po, pml, W, H, G, cap, start, nvalid, window,
-                       a.split_keys, a.nsplit, a.nqblk, scale * 1.4426950408889634f);
+                       (const bf16_t*)kc, (const bf16_t*)vc, po, pml, H, G, cap, row_off, start, window, a.split_keys,
+                       a.nsplit, a.nqblk, scale * 1.4426950408889634f);
     FC_LAUNCH_CHECK();
-    const int64_t items = (int64_t)B * W * H;
-    hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, po, pml,
-                       (bf16_t*)y, B, W, H, G, a.nqblk, a.nsplit, nvalid);
+    hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3(a.nqblk, B * G), dim3(256), 0, s, po, pml, (bf16_t*)y, H, G,
+                       a.nqblk, a.nsplit, row_off);
   } else {
     FC_CHECK_ARG(hd <= 128, "head_dim must be <= 128");
     FC_CHECK_ARG(max_keys <= VALU_MAXK, "VALU attention supports at most 8192 visible keys");
-    const unsigned blocks = (unsigned)(B * W * H);
+    const dim3 grid(max_per_row, H, B);
     if (dtype == FC_BF16)
-      hipLaunchKernelGGL(k_attn_valu<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)q, (const bf16_t*)kc,
-                         (const bf16_t*)vc, (bf16_t*)y, W, H, G, hd, cap, start, nvalid, window, scale);
+      hipLaunchKernelGGL(k_attn_valu<bf16_t>, grid, dim3(256), 0, s, (const bf16_t*)q, (const bf16_t*)kc,
+                         (const bf16_t*)vc, (bf16_t*)y, H, G, hd, cap, row_off, start, window, scale);
     else
-      hipLaunchKernelGGL(k_attn_valu<float>, dim3(blocks), dim3(256), 0, s, (const float*)q, (const float*)kc,
-                         (const float*)vc, (float*)y, W, H, G, hd, cap, start, nvalid, window, scale);
+      hipLaunchKernelGGL(k_attn_valu<float>, grid, dim3(256), 0, s, (const float*)q, (const float*)kc,
+                         (const float*)vc, (float*)y, H, G, hd, cap, row_off, start, window, scale);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
 
-extern "C" int64_t fc_attention_workspace_bytes(int32_t batch, int32_t W, int32_t n_head, int32_t n_kv_head,
-                                                int32_t head_dim, int32_t max_keys) {
-  return fc_attn_part_bytes(batch, W, n_head, n_kv_head, head_dim, max_keys);
+extern "C" int64_t fc_attention_workspace_bytes(int32_t batch, int32_t max_per_row, int32_t n_head,
+                                                int32_t n_kv_head, int32_t head_dim, int32_t max_keys) {
+  return fc_attn_part_bytes(batch, max_per_row, n_head, n_kv_head, head_dim, max_keys);
 }
 
-extern "C" int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y, int32_t batch, int32_t W,
-                                int32_t n_head, int32_t n_kv_head, int32_t head_dim, int32_t cap,
-                                const int32_t* start, const int32_t* nvalid, int32_t window, int32_t max_keys,
-                                int32_t dtype, void* work, int64_t work_bytes, void* stream) {
-  FC_CHECK_ARG(q && kc && vc && y && start && nvalid, "null pointer");
-  FC_CHECK_ARG(batch > 0 && W > 0 && n_head > 0 && n_kv_head > 0, "sizes");
+extern "C" int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y, int32_t batch,
+                                int32_t max_per_row, int32_t n_head, int32_t n_kv_head, int32_t head_dim,
+                                int32_t cap, const int32_t* row_off, const int32_t* start, int32_t window,
+                                int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes, void* stream) {
+  FC_CHECK_ARG(q && kc && vc && y && row_off && start, "null pointer");
+  FC_CHECK_ARG(batch > 0 && max_per_row > 0 && n_head > 0 && n_kv_head > 0, "sizes");
   FC_CHECK_ARG(max_keys > 0 && max_keys <= cap, "max_keys must be in [1, cap]");
-  return fc_launch_attention(q, kc, vc, y, batch, W, n_head, n_kv_head, head_dim, cap, start, nvalid, window,
-                             max_keys, dtype, work, work_bytes, (hipStream_t)stream);
+  return fc_launch_attention(q, kc, vc, y, batch, max_per_row, max_per_row, n_head, n_kv_head, head_dim, cap,
+                             row_off, start, window, max_keys, dtype, work, work_bytes, (hipStream_t)stream);
 }

@@ -21,6 +21,22 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
   return (bf16_t)(u >> 16);
 }
 
+// Fragment order of a bf16 matrix-core operand [R][K] (R padded to a
+// multiple of 16, K a multiple of 32): 16-row x 32-k blocks of 1 KB in
+// [row block][k step] order; inside a block, the 16 bytes at offset 16 l
+// are row l % 16, k = 8 (l / 16) .. +7 of the step, which is exactly what
+// lane l of a 16x16x32 MFMA takes as its operand. One wave-wide 16-byte load
+// then reads 1 KB contiguous. Weights and the bf16 GEMM activations are
+// stored this way; fp32 (parity mode) operands stay row-major.
+__host__ __device__ __forceinline__ int64_t frag_idx(int64_t r, int k, int K) {
+  return ((((r >> 4) * (K >> 5) + (k >> 5)) << 9) | ((int64_t)((r & 15) | (((k & 31) >> 3) << 4)) << 3) |
+          (k & 7));
+}
+template <typename T> __device__ __forceinline__ int64_t act_idx(int64_t r, int k, int K);
+template <> __device__ __forceinline__ int64_t act_idx<uint16_t>(int64_t r, int k, int K) { return frag_idx(r, k, K); }
+template <> __device__ __forceinline__ int64_t act_idx<float>(int64_t r, int k, int K) { return r * K + k; }
+__host__ __device__ __forceinline__ int64_t round16(int64_t r) { return (r + 15) / 16 * 16; }
+
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i);
 template <> __device__ __forceinline__ float ld<float>(const float* p, int64_t i) { return p[i]; }
 template <> __device__ __forceinline__ float ld<bf16_t>(const bf16_t* p, int64_t i) { return bf2f(p[i]); }

@@ -2,9 +2,13 @@
 // the softcapped head, on a preallocated KV cache.
 //
 // One call replaces `_single_step_forward` (flaxchat/engine.py:51-177) for
-// every valid slot of every row at once: the draft's 1-token steps, the
-// target's (k+1)-token verify chunk and prompt prefill are the same code
-// with a different chunk width W. Activations between kernels:
+// every token of every row at once: the draft's 1-token steps, the target's
+// (k+1)-token verify chunk and prompt prefill are the same code with a
+// different chunk. Tokens are packed: row b feeds row_off[b+1] - row_off[b]
+// tokens at consecutive positions from start[b], so rows with more pending
+// tokens cost only their own tokens. The total is a device value; every
+// kernel is launched for the capacity and work past the total exits.
+// Activations between kernels (one row per packed token):
 //   x, x0, xb   fp32 residual stream, x0 and the backout capture
 //   h           RMS-normed GEMM input (model dtype)
 //   qkv         fp32 projections, consumed by the prologue
@@ -14,22 +18,30 @@
 
 #define EMBED_MAXW 1024
 
-// Embedding + RMSNorm + smear (flaxchat/engine.py:80-94). The smear chain
-// x_t = n_t + g_t * x_{t-1} is sequential in t but elementwise in the model
-// dimension, so each thread walks the slots for its own columns.
+// Embedding + RMSNorm + smear (flaxchat/engine.py:80-94), one workgroup per
+// row. The smear chain x_t = n_t + g_t * x_{t-1} is sequential in t but
+// elementwise in the model dimension, so each thread walks the row's tokens
+// for its own columns. Also records the row and position of every packed
+// token for the later per-token kernels.
 template <typename T>
 __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const float* __restrict__ smear_gate,
                                                float smear_lambda, float r0, float a0,
-                                               const int* __restrict__ tokens, const int* __restrict__ start,
-                                               const int* __restrict__ nvalid, int W, int D, int cap,
+                                               const int* __restrict__ tokens, const int* __restrict__ row_off,
+                                               const int* __restrict__ start, int D, int cap,
                                                float* __restrict__ hist, float* __restrict__ x,
-                                               float* __restrict__ x0) {
+                                               float* __restrict__ x0, int* __restrict__ tok_row,
+                                               int* __restrict__ tok_pos) {
   __shared__ float sg[EMBED_MAXW], sinv[EMBED_MAXW];
   const int b = blockIdx.x;
-  const int n = nvalid[b], s0 = start[b], off = W - n;
+  const int base = row_off[b], n = min(row_off[b + 1] - base, EMBED_MAXW), s0 = start[b];
+  if (n <= 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    tok_row[base + j] = b;
+    tok_pos[base + j] = s0 + j;
+  }
   for (int j = wave; j < n; j += 4) {
-    const int tok = tokens[(int64_t)b * W + off + j];
+    const int tok = tokens[base + j];
     const T* e = wte + (int64_t)tok * D;
     float ss = 0.f;
     for (int d = lane; d < D; d += 64) {
@@ -47,18 +59,13 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
   __syncthreads();
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float prev = s0 > 0 ? hist[((int64_t)b * cap + s0 - 1) * D + d] : 0.f;
-    for (int j = 0; j < off; ++j) {
-      const int64_t m = (int64_t)b * W + j;
-      x[m * D + d] = 0.f;
-      x0[m * D + d] = 0.f;
-    }
     for (int j = 0; j < n; ++j) {
-      const int tok = tokens[(int64_t)b * W + off + j];
+      const int tok = tokens[base + j];
       const float nv = ld<T>(wte, (int64_t)tok * D + d) * sinv[j];
       const float xv = nv + sg[j] * prev;
       const int pos = s0 + j;
       if (pos < cap) hist[((int64_t)b * cap + pos) * D + d] = xv;
-      const int64_t m = (int64_t)b * W + off + j;
+      const int64_t m = base + j;
       x0[m * D + d] = xv;
       x[m * D + d] = r0 * xv + a0 * xv;
       prev = xv;
@@ -80,16 +87,27 @@ struct Pending {
 };
 
 // h = x * rsqrt(mean(x^2) + 1e-6) (flaxchat/gpt.py:44-46), after applying a
-// pending update to x. With n_out > 0, output row m reads input row
-// (m / n_out) * W + (W - n_out) + m % n_out (the head only needs the last
-// n_out slots of each row).
+// pending update to x. n_out == 0: one workgroup per packed token (rows past
+// the device total *Mdev exit). n_out > 0 (the head): output row
+// b * n_out + r normalises the token row_off[b+1] - n_out + r, the r-th of
+// row b's last n_out tokens; the residual stream is dead after it, so the
+// finished x is not stored back (a row with fewer than n_out tokens reads a
+// clamped row and its logits are unspecified).
 #define NORM_MAXV 4  // float4 per thread: D <= 4096
 template <typename TO>
-__global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __restrict__ h, int D, int W, int n_out,
-                                                 Pending p) {
+__global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __restrict__ h, int D, int Mcap,
+                                                 const int* __restrict__ Mdev, const int* __restrict__ row_off,
+                                                 int n_out, Pending p) {
   __shared__ float red[16];
   const int row = blockIdx.x, tid = threadIdx.x;
-  const int64_t in_row = n_out > 0 ? (int64_t)(row / n_out) * W + (W - n_out) + row % n_out : row;
+  int64_t in_row = row;
+  if (n_out > 0) {
+    const int b = row / n_out, r = row - b * n_out;
+    in_row = min(max(row_off[b + 1] - n_out + r, 0), Mcap - 1);
+  } else if (Mdev != nullptr && row >= *Mdev) {
+    return;
+  }
+  const bool store_x = n_out == 0;
   const int D4 = D >> 2;
   float4* xr = (float4*)(x + in_row * D);
   float4 v[NORM_MAXV];
@@ -128,7 +146,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __re
             t.z = p.r * t.z + p.a * z.z; t.w = p.r * t.w + p.a * z.w;
           }
         }
-        xr[i] = t;
+        if (store_x) xr[i] = t;
       }
       v[u] = t;
       ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
@@ -136,15 +154,21 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __re
   }
   ss = block_sum(ss, red);
   const float inv = 1.f / sqrtf(ss / (float)D + 1e-6f);
-  TO* hr = h + (int64_t)row * D;
+  // h is the next GEMM's operand: fragment order in bf16 (4 consecutive k
+  // stay contiguous), row-major in fp32
 #pragma unroll
   for (int u = 0; u < NORM_MAXV; ++u) {
     const int i = tid + 256 * u;
     if (i < D4) {
-      st<TO>(hr, 4 * i + 0, v[u].x * inv);
-      st<TO>(hr, 4 * i + 1, v[u].y * inv);
-      st<TO>(hr, 4 * i + 2, v[u].z * inv);
-      st<TO>(hr, 4 * i + 3, v[u].w * inv);
+      const int64_t o = act_idx<TO>(row, 4 * i, D);
+      if constexpr (sizeof(TO) == 2) {
+        uint2 pk;
+        pk.x = (uint32_t)f2bf(v[u].x * inv) | ((uint32_t)f2bf(v[u].y * inv) << 16);
+        pk.y = (uint32_t)f2bf(v[u].z * inv) | ((uint32_t)f2bf(v[u].w * inv) << 16);
+        *(uint2*)(h + o) = pk;
+      } else {
+        *(float4*)(h + o) = make_float4(v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv);
+      }
     }
   }
 }
@@ -152,12 +176,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __re
 struct FwdWork {
   float *x, *x0, *xb, *qkv;
   void *h, *q, *y, *hid, *part;
+  int *tok_row, *tok_pos;
   int64_t part_bytes, total;
   GemmWork gw;
 };
 
-static FwdWork carve(const fc_model* m, int B, int W, int max_keys, char* base) {
-  const int64_t M = (int64_t)B * W;
+// Workspace layout for up to `max_tokens` packed tokens (`typ_tokens`
+// typical) over `B` rows of at most `max_per_row` tokens.
+static FwdWork carve(const fc_model* m, int B, int max_tokens, int max_per_row, int typ_tokens, char* base) {
+  const int64_t M = max_tokens;
   const int D = m->n_embd, H = m->n_head, G = m->n_kv_head, hd = m->head_dim;
   const int es = m->dtype == FC_BF16 ? 2 : 4;
   FwdWork w{};
@@ -171,25 +198,33 @@ static FwdWork carve(const fc_model* m, int B, int W, int max_keys, char* base) 
   w.x0 = (float*)take(M * D * 4);
   w.xb = (float*)take(M * D * 4);
   w.qkv = (float*)take(M * (H + 2 * G) * hd * 4);
-  w.h = take(M * D * es);
+  const int64_t M16 = round16(M);  // GEMM operands in fragment order cover whole 16-row blocks
+  w.h = take(M16 * D * es);
   w.q = take(M * H * hd * es);
-  w.y = take(M * H * hd * es);
-  w.hid = take(M * 4 * D * es);
-  w.part_bytes = fc_attn_part_bytes(B, W, H, G, hd, max_keys);
+  w.y = take(M16 * H * hd * es);
+  w.hid = take(M16 * 4 * D * es);
+  w.tok_row = (int*)take(M * 4);
+  w.tok_pos = (int*)take(M * 4);
+  // attention splits are sized for the largest key range a cache can hold
+  w.part_bytes = fc_attn_part_bytes(B, max_per_row, H, G, hd, 1 << 20);
   w.part = take(w.part_bytes);
   // split-K partials of the two GEMMs that write the residual stream
-  int64_t gp = std::max(fc_gemm_part_bytes((int)M, D, H * hd), fc_gemm_part_bytes((int)M, D, 4 * D));
+  int64_t gp = std::max(fc_gemm_part_bytes(typ_tokens, (int)M, D, H * hd),
+                        fc_gemm_part_bytes(typ_tokens, (int)M, D, 4 * D));
   w.gw.part = (float*)take(gp);
   w.gw.part_bytes = gp;
   w.total = off;
   return w;
 }
 
-extern "C" int64_t fc_forward_workspace_bytes(const fc_model* m, int32_t batch, int32_t W, int32_t n_out) {
-  (void)n_out;
-  if (!m || batch <= 0 || W <= 0) return -1;
-  // attention splits are sized for the largest key range the cache can hold
-  return carve(m, batch, W, 1 << 20, nullptr).total;
+static int typ_of(int max_tokens, int typ_tokens) {
+  return typ_tokens > 0 && typ_tokens <= max_tokens ? typ_tokens : max_tokens;
+}
+
+extern "C" int64_t fc_forward_workspace_bytes(const fc_model* m, int32_t batch, int32_t max_tokens,
+                                              int32_t max_per_row, int32_t typ_tokens) {
+  if (!m || batch <= 0 || max_tokens <= 0 || max_per_row <= 0) return -1;
+  return carve(m, batch, max_tokens, max_per_row, typ_of(max_tokens, typ_tokens), nullptr).total;
 }
 
 static int check_model(const fc_model* m) {
@@ -200,6 +235,8 @@ static int check_model(const fc_model* m) {
   FC_CHECK_ARG(m->n_embd % 8 == 0 && m->n_embd >= 24 && m->n_embd <= 4096,
                "n_embd must be a multiple of 8 in [24, 4096]");
   FC_CHECK_ARG(m->vocab > 0 && m->vocab <= m->vocab_pad, "vocab");
+  FC_CHECK_ARG(m->dtype != FC_BF16 || (m->n_embd % 64 == 0 && m->vocab_pad % 32 == 0),
+               "bf16 needs n_embd % 64 == 0 and vocab_pad % 32 == 0 (fragment-order GEMM operands)");
   return FC_OK;
 }
 
@@ -208,77 +245,86 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   int rc = check_model(m);
   if (rc) return rc;
   FC_CHECK_ARG(c && c->k && c->v && c->hist && c->batch > 0 && c->cap > 0 && c->cap % 32 == 0, "cache");
-  FC_CHECK_ARG(ch && ch->W > 0 && ch->W <= EMBED_MAXW && ch->tokens && ch->start && ch->nvalid, "chunk");
-  FC_CHECK_ARG(ch->n_out >= 0 && ch->n_out <= ch->W, "n_out");
+  FC_CHECK_ARG(ch && ch->tokens && ch->row_off && ch->start, "chunk pointers");
+  FC_CHECK_ARG(ch->max_tokens > 0 && ch->max_per_row > 0 && ch->max_per_row <= EMBED_MAXW &&
+                   ch->max_per_row <= ch->max_tokens,
+               "chunk sizes (max_per_row in [1, 1024] and <= max_tokens)");
+  FC_CHECK_ARG(ch->n_out >= 0 && ch->n_out <= ch->max_per_row, "n_out");
+  FC_CHECK_ARG((int64_t)c->batch * ch->n_out <= ch->max_tokens, "batch * n_out must not exceed max_tokens");
   FC_CHECK_ARG(ch->n_out == 0 || ch->logits, "logits pointer");
   hipStream_t s = (hipStream_t)stream;
-  const int B = c->batch, W = ch->W, M = B * W;
+  const int B = c->batch, Mcap = ch->max_tokens, Mtyp = typ_of(Mcap, ch->typ_tokens);
+  const int* Mdev = ch->row_off + B;
   const int D = m->n_embd, H = m->n_head, G = m->n_kv_head, hd = m->head_dim;
   const int NQKV = (H + 2 * G) * hd;
-  FwdWork w = carve(m, B, W, 1 << 20, (char*)work);
+  FwdWork w = carve(m, B, Mcap, ch->max_per_row, Mtyp, (char*)work);
   FC_CHECK_ARG(work && work_bytes >= w.total, "forward workspace too small");
   const int dt = m->dtype;
   const int64_t layer_elems = (int64_t)B * G * c->cap * hd;
   const int es = dt == FC_BF16 ? 2 : 4;
+  const int typ_per_row = std::max(1, (Mtyp + B - 1) / B);
 
   if (dt == FC_BF16)
     hipLaunchKernelGGL(k_embed<bf16_t>, dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
-                       m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->start,
-                       ch->nvalid, W, D, c->cap, c->hist, w.x, w.x0);
+                       m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
+                       ch->start, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
   else
     hipLaunchKernelGGL(k_embed<float>, dim3(B), dim3(256), 0, s, (const float*)m->wte, m->smear_gate,
-                       m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->start,
-                       ch->nvalid, W, D, c->cap, c->hist, w.x, w.x0);
+                       m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
+                       ch->start, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
   FC_LAUNCH_CHECK();
 
   Pending pend{};
   auto norm = [&](int rows, int n_out) {
+    const int* md = n_out > 0 ? nullptr : Mdev;
     if (dt == FC_BF16)
-      hipLaunchKernelGGL(k_rmsnorm<bf16_t>, dim3(rows), dim3(256), 0, s, w.x, (bf16_t*)w.h, D, W, n_out, pend);
+      hipLaunchKernelGGL(k_rmsnorm<bf16_t>, dim3(rows), dim3(256), 0, s, w.x, (bf16_t*)w.h, D, Mcap, md, ch->row_off,
+                         n_out, pend);
     else
-      hipLaunchKernelGGL(k_rmsnorm<float>, dim3(rows), dim3(256), 0, s, w.x, (float*)w.h, D, W, n_out, pend);
+      hipLaunchKernelGGL(k_rmsnorm<float>, dim3(rows), dim3(256), 0, s, w.x, (float*)w.h, D, Mcap, md, ch->row_off,
+                         n_out, pend);
     pend = Pending{};
   };
   const int backout = m->n_layer / 2;
   for (int l = 0; l < m->n_layer; ++l) {
     const fc_layer& L = m->layers[l];
-    norm(M, 0);
+    norm(Mcap, 0);
     FC_LAUNCH_CHECK();
     Epi e{};
     e.mode = EPI_STORE;
     e.out = w.qkv;
     e.ldo = NQKV;
-    rc = fc_launch_gemm(w.h, L.wqkv, M, NQKV, D, dt, e, w.gw, s, nullptr);
+    rc = fc_launch_gemm(w.h, L.wqkv, Mcap, Mdev, Mtyp, NQKV, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
-    rc = fc_launch_prologue(w.qkv, w.h, ch->tokens, m, l, c, ch->start, ch->nvalid, B, W, w.q, s);
+    rc = fc_launch_prologue(w.qkv, w.h, ch->tokens, m, l, c, w.tok_row, w.tok_pos, Mcap, Mdev, w.q, s);
     if (rc) return rc;
     int max_keys = c->cap;
-    if (L.window > 0) max_keys = std::min(c->cap, L.window + W);
+    if (L.window > 0) max_keys = std::min(c->cap, L.window + ch->max_per_row);
     rc = fc_launch_attention(w.q, (const char*)c->k + layer_elems * l * es, (const char*)c->v + layer_elems * l * es,
-                             w.y, B, W, H, G, hd, c->cap, ch->start, ch->nvalid, L.window, max_keys, dt, w.part,
-                             w.part_bytes, s);
+                             w.y, B, ch->max_per_row, typ_per_row, H, G, hd, c->cap, ch->row_off, ch->start, L.window,
+                             max_keys, dt, w.part, w.part_bytes, s);
     if (rc) return rc;
     e = Epi{};
     e.mode = EPI_ADD;
     e.out = w.x;
     e.ldo = D;
     int S = 1;
-    rc = fc_launch_gemm(w.y, L.wo, M, D, H * hd, dt, e, w.gw, s, &S);
+    rc = fc_launch_gemm(w.y, L.wo, Mcap, Mdev, Mtyp, D, H * hd, dt, e, w.gw, s, &S);
     if (rc) return rc;
     if (S > 1) {
       pend.S = S;
       pend.mode = EPI_ADD;
-      pend.rows = M;
+      pend.rows = Mcap;
       pend.part = w.gw.part;
     }
-    norm(M, 0);
+    norm(Mcap, 0);
     FC_LAUNCH_CHECK();
     e = Epi{};
     e.mode = EPI_RELU2;
     e.out = w.hid;
     e.ldo = 4 * D;
     e.out_dtype = dt;
-    rc = fc_launch_gemm(w.h, L.wfc, M, 4 * D, D, dt, e, w.gw, s, nullptr);
+    rc = fc_launch_gemm(w.h, L.wfc, Mcap, Mdev, Mtyp, 4 * D, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
     e = Epi{};
     e.mode = EPI_MLPOUT;
@@ -294,12 +340,12 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
       e.a = m->layers[l + 1].x0_lambda;
     }
     S = 1;
-    rc = fc_launch_gemm(w.hid, L.wproj, M, D, 4 * D, dt, e, w.gw, s, &S);
+    rc = fc_launch_gemm(w.hid, L.wproj, Mcap, Mdev, Mtyp, D, 4 * D, dt, e, w.gw, s, &S);
     if (rc) return rc;
     if (S > 1) {
       pend.S = S;
       pend.mode = EPI_MLPOUT;
-      pend.rows = M;
+      pend.rows = Mcap;
       pend.part = w.gw.part;
       pend.x0 = w.x0;
       pend.xb = w.xb;
@@ -320,7 +366,7 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.n_out = ch->n_out;
     e.row_stride = ch->logits_stride;
     e.V = m->vocab;
-    rc = fc_launch_gemm(w.h, m->lm_head, Mo, m->vocab_pad, D, dt, e, w.gw, s, nullptr);
+    rc = fc_launch_gemm(w.h, m->lm_head, Mo, nullptr, Mo, m->vocab_pad, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
   }
   return FC_OK;

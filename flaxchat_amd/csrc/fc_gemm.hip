@@ -7,20 +7,16 @@
 // layer (engine.py:94), the backout capture and subtraction
 // (engine.py:164-166) and the 15*tanh(z/15) softcap (engine.py:173-174).
 //
-// Kernels, chosen by M (= rows = batch x tokens per row):
-//   k_gemv        VALU dot products; fp32 weights (parity mode) or bf16 with
-//                 M < 16, where a 16-row matrix-core tile would be mostly empty.
-//   k_gemm_stream bf16 MFMA 16x16x32 for M <= 64 (draft steps): pure weight
-//                 streaming. A workgroup owns 16 output columns; its four
-//                 waves split K and each wave issues the 16-byte weight loads
-//                 of up to four 128-wide k chunks before the first MFMA, so
-//                 ~16 KB per wave are in flight; the activation rows come
-//                 straight from L2.
-//   k_gemm_tile   bf16 MFMA for M > 64 (verify / prefill). A workgroup owns
-//                 up to 256 rows x 128 columns; the activation chunk is staged
-//                 in LDS (double buffered) and each wave reuses every A
-//                 fragment for two 16-column blocks, halving LDS traffic per
-//                 MFMA; weight fragments for the next chunk are prefetched.
+// Kernels:
+//   k_gemv     VALU dot products: fp32 weights (parity mode), or bf16 with
+//              fewer than 8 rows, where a 16-row matrix-core tile would be
+//              mostly empty.
+//   k_gemm_ks  bf16 MFMA 16x16x32 for everything else (draft steps, verify,
+//              prefill, lm_head): workgroup tile of 16-64 rows x 16-64
+//              columns, the four waves split K, deep register prefetch.
+// The row count may be a device value (packed token chunks whose size is
+// only known on the GPU): the grid covers the capacity and tiles past the
+// actual count exit at once.
 // When N alone gives too few workgroups to occupy 256 CUs, a GEMM whose
 // output is the fp32 residual stream may split K across workgroups: each
 // split writes its partial product with plain stores and the RMSNorm kernel
@@ -38,10 +34,10 @@ __device__ __forceinline__ void epi_apply(const Epi e, int m, int n, float acc) 
   } else if constexpr (EPI == EPI_ADD) {
     float* o = (float*)e.out + (int64_t)m * e.ldo + n;
     *o = *o + acc;
-  } else if constexpr (EPI == EPI_RELU2) {
+  } else if constexpr (EPI == EPI_RELU2) {  // the next GEMM's operand: fragment order in bf16
     float r = fmaxf(acc, 0.f);
     r = r * r;
-    if (e.out_dtype == FC_BF16) ((bf16_t*)e.out)[(int64_t)m * e.ldo + n] = f2bf(r);
+    if (e.out_dtype == FC_BF16) ((bf16_t*)e.out)[frag_idx(m, n, (int)e.ldo)] = f2bf(r);
     else ((float*)e.out)[(int64_t)m * e.ldo + n] = r;
   } else if constexpr (EPI == EPI_MLPOUT) {
     const int64_t i = (int64_t)m * e.ldo + n;
@@ -89,12 +85,14 @@ __device__ __forceinline__ void load_vec<bf16_t, 8>(const bf16_t* p, float* o) {
 }
 
 template <typename T, int MB, int EPI>
-__global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* __restrict__ W, int M, int N,
-                                              int K, Epi e) {
+__global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* __restrict__ W, int Mcap,
+                                              const int* __restrict__ Mdev, int N, int K, Epi e) {
   constexpr int VEC = 16 / sizeof(T);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * 4;
   const int m0 = blockIdx.y * MB;
+  const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
+  if (m0 >= M) return;
   float acc[MB][4];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -147,167 +145,139 @@ __device__ __forceinline__ f32x4 mfma16(v4u a, v4u b, f32x4 c) {
                                                   0, 0);
 }
 
-// M <= 64: streaming. grid (N/64, S, ceil(M/(16 MB))). A workgroup owns 64
-// columns (4 N-blocks) so each activation fragment fetched from L2 feeds four
-// MFMAs; its four waves split K in 128-wide chunks and each wave keeps two
-// chunks of weight fragments (32 KB per wave) in flight.
-template <int MB, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_stream(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
-                                                     int M, int N, int K, int S, Epi e) {
-  constexpr int NB = 4, U = 2;
+// bf16 MFMA GEMM, K split over the four waves of a workgroup.
+//
+// A workgroup owns an MT x NT output tile (MT = 16 MB rows, NT = 16 NB
+// columns) over its split's K range; its four waves take interleaved
+// 64-wide k chunks, so every weight and activation byte reaches the CU once
+// and no LDS traffic or barrier sits in the main loop. Each wave keeps NS
+// chunks of A and W fragments in flight in registers (the loads of chunk
+// i + NS are issued right after chunk i is consumed). The four partial
+// tiles are summed in LDS at the end and the epilogue runs on a coalesced
+// row-major layout.
+//
+// Grid: 1-D over (N tile, K split, M tile). Workgroups are dealt to the
+// eight XCDs round robin, so N tile n lands on XCD n % 8 and, within an XCD,
+// the M tiles of one N tile are consecutive: the weight slab they share is
+// read from HBM once and hit in that XCD's L2 by the others. The row count
+// may live on the device (`Mdev`, at most Mcap): tiles past it exit at once.
+template <int MB, int NB, int NS, int EPI, bool PK = false>
+__global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                 int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
+                                                 int S, int mtiles, Epi e) {
+  constexpr int MT = 16 * MB, NT = 16 * NB;
+  const int id = blockIdx.x;
+  const int xcd = id & 7, loc = id >> 3;
+  const int per = S * mtiles;
+  const int nl = loc / per, rem = loc - nl * per;
+  const int s = rem / mtiles, mt = rem - s * mtiles;
+  const int nt = nl * 8 + xcd;
+  if (nt >= ntiles) return;
+  const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
+  const int m0 = mt * MT;
+  if (m0 >= M) return;
+  const int n0 = nt * NT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 64;
-  const int s = blockIdx.y;
-  const int m0 = blockIdx.z * 16 * MB;
-  const int C = K >> 7;
+  const int C = K >> 6;
   const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
+  const int nch = c_end - c_beg > wave ? (c_end - c_beg - wave + 3) >> 2 : 0;
+
   f32x4 acc[MB][NB];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bf16_t* wbase = W + (int64_t)(n0 + r) * K + 8 * g;
-  const bf16_t* abase[MB];
+  // operand addresses at k = 0. Row-major: lane l reads row (l % 16), 16 B
+  // at k = 8 (l / 16). Fragment order (PK): 16-row x 32-k blocks of 1 KB in
+  // [row block][k step] order, lane l's 16 B at offset 16 l of its block,
+  // so each load instruction reads 1 KB contiguous. Either way the chunk
+  // offset of k step t is `kstep_elems * t`.
+  const bf16_t* wrow[NB];
+  const bf16_t* arow[MB];
+  int64_t kstep_elems;
+  if constexpr (PK) {
+    const int64_t KS32 = K >> 5;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) abase[mb] = A + (int64_t)min(m0 + 16 * mb + r, M - 1) * K + 8 * g;
-  for (int c0 = c_beg + wave; c0 < c_end; c0 += 4 * U) {
-    v4u wf[U][NB][4];
+    for (int j = 0; j < NB; ++j) wrow[j] = W + (int64_t)(n0 / 16 + j) * KS32 * 512 + lane * 8;
+    const int last_blk = (M - 1) >> 4;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = min(c0 + 4 * u, c_end - 1);  // a clamped duplicate chunk is loaded, never used
+    for (int i = 0; i < MB; ++i) arow[i] = A + (int64_t)min(m0 / 16 + i, last_blk) * KS32 * 512 + lane * 8;
+    kstep_elems = 512;
+  } else {
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
+    for (int j = 0; j < NB; ++j) wrow[j] = W + (int64_t)(n0 + 16 * j + r) * K + 8 * g;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) wf[u][j][st] = *(const v4u*)(wbase + (int64_t)16 * j * K + c * 128 + 32 * st);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + 4 * u;
-      if (c < c_end) {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          v4u af[4];
-#pragma unroll
-          for (int st = 0; st < 4; ++st) af[st] = *(const v4u*)(abase[mb] + c * 128 + 32 * st);
-#pragma unroll
-          for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int j = 0; j < NB; ++j) acc[mb][j] = mfma16(af[st], wf[u][j][st], acc[mb][j]);
-        }
-      }
-    }
+    for (int i = 0; i < MB; ++i) arow[i] = A + (int64_t)min(m0 + 16 * i + r, M - 1) * K + 8 * g;
+    kstep_elems = 32;
   }
-  __shared__ f32x4 red[3][MB * NB][64];
-  if (wave > 0)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < NB; ++j) red[wave - 1][mb * NB + j][lane] = acc[mb][j];
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int w = 0; w < 3; ++w) acc[mb][j] += red[w][mb * NB + j][lane];
-  }
-  Epi ee = e;
-  ee.split = s;
-  if (wave == 0) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = m0 + 16 * mb + 4 * g + i;
-          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * j + r, acc[mb][j][i]);
-        }
-  }
-}
 
-// M > 64: LDS-staged activations. grid (N/128, S, ceil(M/(16 MB))).
-template <int MB, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_tile(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
-                                                   int M, int N, int K, int S, Epi e) {
-  constexpr int NB = 2, KC = 64, LDA = KC + 8, ROWS = 16 * MB;
-  constexpr int PASSES = ROWS / 32;  // 32 rows x 64 k per 256-thread pass
-  static_assert(ROWS % 32 == 0, "tile rows must be a multiple of 32");
-  __shared__ bf16_t As[2][ROWS * LDA];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  const int nw = blockIdx.x * 128 + wave * 32;
-  const int s = blockIdx.y;
-  const int m0 = blockIdx.z * ROWS;
-  const int C = K / KC;
-  const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
-  f32x4 acc[MB][NB];
-#pragma unroll
-  for (int i = 0; i < MB; ++i)
-#pragma unroll
-    for (int j = 0; j < NB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint4 zero = {0u, 0u, 0u, 0u};
-  const int srow = t >> 3, scol = (t & 7) * 8;
-  const bf16_t* w0 = W + (int64_t)(nw + r) * K + 8 * g;
-  const bf16_t* w1 = w0 + (int64_t)16 * K;
+  if (nch > 0) {
+    static_assert(NS == 2, "the pipeline below is written for two stages");
+    v4u wb0[NB][2], ab0[MB][2], wb1[NB][2], ab1[MB][2];
+    // chunk index of the wave's i-th chunk, clamped so the tail loads are
+    // harmless re-reads and the loop body has no branch
+#define KS_LOAD(wb, ab, i)                                                          \
+  {                                                                                 \
+    const int c_ = c_beg + wave + 4 * min((i), nch - 1);                            \
+    _Pragma("unroll") for (int j = 0; j < NB; ++j)                                  \
+      _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
+        wb[j][ks] = *(const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems);           \
+    _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                               \
+      _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
+        ab[mb][ks] = *(const v4u*)(arow[mb] + (2 * c_ + ks) * kstep_elems);         \
+  }
+#define KS_MMA(wb, ab)                                                              \
+  {                                                                                 \
+    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                                \
+      _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                             \
+        _Pragma("unroll") for (int j = 0; j < NB; ++j)                              \
+          acc[mb][j] = mfma16(ab[mb][ks], wb[j][ks], acc[mb][j]);                   \
+  }
+    KS_LOAD(wb0, ab0, 0);
+    KS_LOAD(wb1, ab1, 1);
+    int i = 0;
+    // the scheduling barriers keep each chunk's loads together and after the
+    // MFMAs that free its registers, so the other stage's loads stay in
+    // flight while a stage computes (the waits become vmcnt(one stage))
+    for (; i + 1 < nch; i += 2) {
+      KS_MMA(wb0, ab0);
+      __builtin_amdgcn_sched_barrier(0);
+      KS_LOAD(wb0, ab0, i + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      KS_MMA(wb1, ab1);
+      __builtin_amdgcn_sched_barrier(0);
+      KS_LOAD(wb1, ab1, i + 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < nch) KS_MMA(wb0, ab0);
+#undef KS_LOAD
+#undef KS_MMA
+  }
 
-  v4u ast[PASSES];
-  v4u wc0[2], wc1[2], wn0[2], wn1[2];
-  // prologue: chunk c_beg (every split owns >= 1 chunk)
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p)
-    ast[p] = *(const v4u*)(A + (int64_t)min(m0 + srow + 32 * p, M - 1) * K + c_beg * KC + scol);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    wc0[ks] = *(const v4u*)(w0 + c_beg * KC + 32 * ks);
-    wc1[ks] = *(const v4u*)(w1 + c_beg * KC + 32 * ks);
-  }
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) *(v4u*)(&As[0][(srow + 32 * p) * LDA + scol]) = ast[p];
-  for (int c = c_beg; c < c_end; ++c) {
-    const int buf = (c - c_beg) & 1;
-    // prefetch the next chunk unconditionally (the last iteration re-reads its
-    // own chunk) so the staging registers never live across a branch; rows
-    // past M are clamped: computed, never stored
-    const int cn = min(c + 1, c_end - 1);
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-      ast[p] = *(const v4u*)(A + (int64_t)min(m0 + srow + 32 * p, M - 1) * K + cn * KC + scol);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      wn0[ks] = *(const v4u*)(w0 + cn * KC + 32 * ks);
-      wn1[ks] = *(const v4u*)(w1 + cn * KC + 32 * ks);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const v4u af = *(const v4u*)(&As[buf][(16 * mb + r) * LDA + 32 * ks + 8 * g]);
-        acc[mb][0] = mfma16(af, wc0[ks], acc[mb][0]);
-        acc[mb][1] = mfma16(af, wc1[ks], acc[mb][1]);
-      }
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) *(v4u*)(&As[buf ^ 1][(srow + 32 * p) * LDA + scol]) = ast[p];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      wc0[ks] = wn0[ks];
-      wc1[ks] = wn1[ks];
-    }
-  }
-  Epi ee = e;
-  ee.split = s;
+  // sum the four waves' tiles; thread t then owns OPT consecutive columns
+  // of one row
+  constexpr int LDR = NT + 4, OPT = MT * NT / 256, TPR = NT / OPT;
+  static_assert(OPT >= 1 && NT % OPT == 0, "epilogue tiling");
+  __shared__ float red[4][MT][LDR];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 16 * mb + 4 * g + i;
-        if (m < M) epi_apply<EPI>(ee, m, nw + 16 * j + r, acc[mb][j][i]);
-      }
+      for (int i = 0; i < 4; ++i) red[wave][16 * mb + 4 * g + i][16 * j + r] = acc[mb][j][i];
+  __syncthreads();
+  const int t = threadIdx.x;
+  const int row = t / TPR, col0 = (t - row * TPR) * OPT;
+  const int m = m0 + row;
+  if (m >= M) return;
+  Epi ee = e;
+  ee.split = s;
+#pragma unroll
+  for (int c = 0; c < OPT; ++c) {
+    const float v = red[0][row][col0 + c] + red[1][row][col0 + c] + red[2][row][col0 + c] + red[3][row][col0 + c];
+    epi_apply<EPI>(ee, m, n0 + col0 + c, v);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -324,109 +294,105 @@ __global__ __launch_bounds__(256) void k_gemm_tile(const bf16_t* __restrict__ A,
   }
 
 template <typename T, int MB>
-static void launch_gemv_mb(const void* A, const void* W, int M, int N, int K, const Epi& e, hipStream_t s) {
+static void launch_gemv_mb(const void* A, const void* W, int M, const int* Mdev, int N, int K, const Epi& e,
+                           hipStream_t s) {
   const dim3 grid((N + 15) / 16, (M + MB - 1) / MB);
   FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemv<T, MB, E>), grid, dim3(256), 0, s, (const T*)A, (const T*)W, M,
-                                           N, K, e));
+                                           Mdev, N, K, e));
 }
 template <typename T>
-static void launch_gemv(const void* A, const void* W, int M, int N, int K, const Epi& e, hipStream_t s) {
-  if (M <= 1) launch_gemv_mb<T, 1>(A, W, M, N, K, e, s);
-  else if (M <= 2) launch_gemv_mb<T, 2>(A, W, M, N, K, e, s);
-  else if (M <= 4) launch_gemv_mb<T, 4>(A, W, M, N, K, e, s);
-  else launch_gemv_mb<T, 8>(A, W, M, N, K, e, s);
+static void launch_gemv(const void* A, const void* W, int M, const int* Mdev, int N, int K, const Epi& e,
+                        hipStream_t s) {
+  if (M <= 1) launch_gemv_mb<T, 1>(A, W, M, Mdev, N, K, e, s);
+  else if (M <= 2) launch_gemv_mb<T, 2>(A, W, M, Mdev, N, K, e, s);
+  else if (M <= 4) launch_gemv_mb<T, 4>(A, W, M, Mdev, N, K, e, s);
+  else launch_gemv_mb<T, 8>(A, W, M, Mdev, N, K, e, s);
 }
 
-template <int MB>
-static void launch_stream(const void* A, const void* W, int M, int N, int K, int S, const Epi& e, hipStream_t s) {
-  const dim3 grid(N / 64, S, (M + 16 * MB - 1) / (16 * MB));
-  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_stream<MB, E>), grid, dim3(256), 0, s, (const bf16_t*)A,
-                                           (const bf16_t*)W, M, N, K, S, e));
-}
-template <int MB>
-static void launch_tile(const void* A, const void* W, int M, int N, int K, int S, const Epi& e, hipStream_t s) {
-  const dim3 grid(N / 128, S, (M + 16 * MB - 1) / (16 * MB));
-  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_tile<MB, E>), grid, dim3(256), 0, s, (const bf16_t*)A,
-                                           (const bf16_t*)W, M, N, K, S, e));
+#define FC_GEMM_NS 2
+template <int MB, int NB, bool PK = false>
+static void launch_ks(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int S, const Epi& e,
+                      hipStream_t s) {
+  const int ntiles = N / (16 * NB), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
+  const int nwg = (ntiles + 7) / 8 * 8 * S * mtiles;
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_ks<MB, NB, FC_GEMM_NS, E, PK>), dim3(nwg), dim3(256), 0, s,
+                                           (const bf16_t*)A, (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, S, mtiles,
+                                           e));
 }
 
-// split count so that (workgroups x S) reaches ~2 per CU, keeping >= min_chunks
-// chunks per split
-// split count so that (workgroups x S) reaches ~2 per CU, keeping >= 1 chunk
-// per split
-static int pick_split(int wgs, int chunks) {
-  if (wgs <= 0 || chunks <= 0) return 1;
-  int S = (256 + wgs - 1) / wgs;
-  return std::max(1, std::min(std::min(S, chunks), FC_MAX_SPLIT));
-}
-
-// One plan drives the workspace sizing and the launch.
-enum { GK_GEMV = 0, GK_STREAM = 1, GK_TILE = 2 };
+// One plan drives the workspace sizing and the launch. The tile shape and
+// the K split are chosen for the typical row count Mtyp (the grid covers
+// Mcap rows; tiles past the device-side count exit at once).
 struct GemmPlan {
-  int kind, mb, mtiles, ntiles, S;
+  bool gemv;
+  int mb, nb, S;
 };
-static GemmPlan plan_gemm(int M, int N, int K, int dtype, bool can_split) {
+static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
   GemmPlan p{};
   p.S = 1;
-  if (dtype == FC_F32 || M < 16 || K % 128 != 0 || N % 64 != 0) {
-    p.kind = GK_GEMV;
+  if (dtype == FC_F32) {
+    p.gemv = true;
     return p;
   }
-  if (M <= 64 || N % 128 != 0) {
-    p.kind = GK_STREAM;
-    p.mb = std::min(4, (M + 15) / 16);
-    p.mtiles = (M + 16 * p.mb - 1) / (16 * p.mb);
-    p.ntiles = N / 64;
-    if (can_split) p.S = pick_split(p.ntiles * p.mtiles, K / 128);
-  } else {
-    p.kind = GK_TILE;
-    p.ntiles = N / 128;
-    // wide N: one M tile streams the weights exactly once; narrower N: 64-row
-    // M tiles multiply the workgroups (weight re-reads hit L2 / MALL)
-    if (p.ntiles >= 128) p.mb = M <= 128 ? 8 : (M <= 192 ? 12 : (M <= 224 ? 14 : 16));
-    else p.mb = 4;
-    p.mtiles = (M + 16 * p.mb - 1) / (16 * p.mb);
-    if (can_split) p.S = pick_split(p.ntiles * p.mtiles, K / 64);
+  p.mb = Mtyp <= 16 ? 1 : (Mtyp <= 32 ? 2 : 4);
+  const int mtiles = (Mtyp + 16 * p.mb - 1) / (16 * p.mb);
+  // widest column tile that still gives >= 256 workgroups, else the
+  // narrowest allowed one plus a K split when the output allows it
+  const int nb_min = p.mb == 2 ? 1 : 2;
+  p.nb = nb_min;
+  for (int nb = 4; nb >= nb_min; nb /= 2)
+    if (N % (16 * nb) == 0 && (N / (16 * nb)) * mtiles >= 256) {
+      p.nb = nb;
+      break;
+    }
+  if (N % (16 * p.nb) != 0) p.nb = 2;
+  const int wgs = (N / (16 * p.nb)) * mtiles;
+  if (can_split && wgs < 256) {
+    const int C = K / 64;
+    int S = (256 + wgs - 1) / wgs;
+    S = std::min(S, std::max(1, C / 4));  // keep >= 1 chunk per wave
+    p.S = std::max(1, std::min(S, FC_MAX_SPLIT));
   }
   return p;
 }
 
-int64_t fc_gemm_part_bytes(int M, int N, int K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  GemmPlan p = plan_gemm(M, N, K, FC_BF16, true);
-  return p.S > 1 ? fc_align((int64_t)p.S * M * N * 4) : 0;
+int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K) {
+  if (Mtyp <= 0 || Mcap <= 0 || N <= 0 || K <= 0) return 0;
+  GemmPlan p = plan_gemm(Mtyp, N, K, FC_BF16, true);
+  return p.S > 1 ? fc_align((int64_t)p.S * Mcap * N * 4) : 0;
 }
 
-int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, const GemmWork& gw,
-                   hipStream_t s, int* splits) {
+int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int Mtyp, int N, int K, int dtype,
+                   const Epi& e, const GemmWork& gw, hipStream_t s, int* splits) {
   if (splits) *splits = 1;
-  if (M <= 0 || N <= 0) return FC_OK;
+  if (Mcap <= 0 || N <= 0) return FC_OK;
   FC_CHECK_ARG(K > 0 && K % 8 == 0, "gemm K must be a positive multiple of 8");
+  if (Mtyp <= 0 || Mtyp > Mcap) Mtyp = Mcap;
+  FC_CHECK_ARG(dtype == FC_F32 || (K % 64 == 0 && N % 32 == 0),
+               "bf16 GEMM needs K % 64 == 0 and N % 32 == 0 (fragment-order operands)");
   const bool can_split = splits != nullptr && gw.part != nullptr;
-  GemmPlan p = plan_gemm(M, N, K, dtype, can_split);
-  if (p.S > 1 && (int64_t)p.S * M * N * 4 > gw.part_bytes) p.S = 1;
+  GemmPlan p = plan_gemm(Mtyp, N, K, dtype, can_split);
+  if (p.S > 1 && (int64_t)p.S * Mcap * N * 4 > gw.part_bytes) p.S = 1;
   Epi ee = e;
   if (p.S > 1) {
     ee.mode = EPI_PARTIAL;
     ee.part = gw.part;
-    ee.part_rows = M;
+    ee.part_rows = Mcap;
     ee.ldo = N;
     *splits = p.S;
   }
-  if (p.kind == GK_GEMV) {
-    if (dtype == FC_F32) launch_gemv<float>(A, W, M, N, K, ee, s);
-    else launch_gemv<bf16_t>(A, W, M, N, K, ee, s);
-  } else if (p.kind == GK_STREAM) {
-    if (p.mb == 1) launch_stream<1>(A, W, M, N, K, p.S, ee, s);
-    else if (p.mb == 2) launch_stream<2>(A, W, M, N, K, p.S, ee, s);
-    else if (p.mb == 3) launch_stream<3>(A, W, M, N, K, p.S, ee, s);
-    else launch_stream<4>(A, W, M, N, K, p.S, ee, s);
+  if (p.gemv) {
+    launch_gemv<float>(A, W, Mcap, Mdev, N, K, ee, s);
+  } else if (p.mb == 1) {
+    if (p.nb == 4) launch_ks<1, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+    else launch_ks<1, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+  } else if (p.mb == 2) {
+    if (p.nb == 4) launch_ks<2, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+    else if (p.nb == 2) launch_ks<2, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+    else launch_ks<2, 1, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
   } else {
-    if (p.mb == 4) launch_tile<4>(A, W, M, N, K, p.S, ee, s);
-    else if (p.mb == 8) launch_tile<8>(A, W, M, N, K, p.S, ee, s);
-    else if (p.mb == 12) launch_tile<12>(A, W, M, N, K, p.S, ee, s);
-    else if (p.mb == 14) launch_tile<14>(A, W, M, N, K, p.S, ee, s);
-    else launch_tile<16>(A, W, M, N, K, p.S, ee, s);
+    if (p.nb == 4) launch_ks<4, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+    else launch_ks<4, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
@@ -445,5 +411,34 @@ extern "C" int32_t fc_gemm(const void* A, const void* W, void* out, int32_t M, i
   e.n_out = 1;
   e.row_stride = N;
   e.V = N;
-  return fc_launch_gemm(A, W, M, N, K, dtype, e, GemmWork{}, (hipStream_t)stream, nullptr);
+  return fc_launch_gemm(A, W, M, nullptr, M, N, K, dtype, e, GemmWork{}, (hipStream_t)stream, nullptr);
+}
+
+// Fragment-order copy of a row-major bf16 matrix src[rows][K] into
+// dst[round16(rows)][K] (padding rows zero); one thread per 16-byte group.
+__global__ __launch_bounds__(256) void k_pack_frag(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst,
+                                                   int rows, int K) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t groups = round16(rows) * (K / 8);
+  if (t >= groups) return;
+  const int64_t blk = t >> 6;  // 64 groups per 16 x 32 block
+  const int lane = (int)(t & 63);
+  const int KS = K >> 5;
+  const int64_t rb = blk / KS;
+  const int ks = (int)(blk - rb * KS);
+  const int64_t r = rb * 16 + (lane & 15);
+  const int k = ks * 32 + (lane >> 4) * 8;
+  uint4 v = {0u, 0u, 0u, 0u};
+  if (r < rows) v = *(const uint4*)(src + r * K + k);
+  *(uint4*)(dst + t * 8) = v;
+}
+
+extern "C" int32_t fc_pack_operand(const void* src, void* dst, int32_t rows, int32_t K, void* stream) {
+  FC_CHECK_ARG(src && dst && src != dst, "pointers (distinct, non-null)");
+  FC_CHECK_ARG(rows > 0 && K > 0 && K % 32 == 0, "rows > 0 and K % 32 == 0");
+  const int64_t groups = round16(rows) * (K / 8);
+  hipLaunchKernelGGL(k_pack_frag, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const bf16_t*)src, (bf16_t*)dst, rows, K);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
 }

@@ -30,20 +30,22 @@ struct GemmWork {
   float* part;
   int64_t part_bytes;
 };
-int64_t fc_gemm_part_bytes(int M, int N, int K);
+int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K);
 // `splits` (may be NULL: no split) receives the split count; when > 1 the
 // output was written as partials to gw.part and the caller must finish it.
-int fc_launch_gemm(const void* A, const void* W, int M, int N, int K, int dtype, const Epi& e, const GemmWork& gw,
+int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int Mtyp, int N, int K, int dtype,
+                   const Epi& e, const GemmWork& gw,
                    hipStream_t s, int* splits);
 
 struct AttnGrid {
   int nqblk, nsplit, split_keys;
 };
-AttnGrid fc_attn_grid(int batch, int W, int n_head, int n_kv_head, int max_keys);
-int64_t fc_attn_part_bytes(int batch, int W, int n_head, int n_kv_head, int head_dim, int max_keys);
-int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int W, int H, int G, int hd,
-                        int cap, const int* start, const int* nvalid, int window, int max_keys, int dtype,
-                        void* part, int64_t part_bytes, hipStream_t s);
+AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, int n_kv_head, int max_keys);
+int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head, int head_dim, int max_keys);
+int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_per_row,
+                        int typ_per_row, int H, int G, int hd, int cap, const int* row_off, const int* start,
+                        int window, int max_keys, int dtype, void* part, int64_t part_bytes, hipStream_t s);
 int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const fc_model* m, int layer,
-                       const fc_cache* c, const int* start, const int* nvalid, int B, int W, void* q, hipStream_t s);
+                       const fc_cache* c, const int* tok_row, const int* tok_pos, int Mcap, const int* Mdev, void* q,
+                       hipStream_t s);
 int fc_launch_row_stats(const float* logits, int rows, int V, float T, int top_k, fc_rowstat* stats, hipStream_t s);

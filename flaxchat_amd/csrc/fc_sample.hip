@@ -244,8 +244,8 @@ struct SpecDev {  // the fc_spec_state fields the kernels read, by value
   int top_k;
   uint64_t seed;
   int *t_len, *d_len, *t_pend, *d_pend, *t_pend_n, *d_pend_n, *t_dirty, *d_dirty, *gen, *gen_n, *prompt_len,
-      *round, *result;
-  int *tok_d0, *n_d0, *start_d, *tok_ds, *ones, *tok_v, *start_v, *n_v, *drafts;
+      *round, *stall, *result;
+  int *tok_d0, *off_d0, *start_d, *tok_ds, *off_ds, *tok_v, *off_v, *start_v, *drafts;
   float *q_logits, *p_logits;
   fc_rowstat *q_stats, *p_stats;
 };
@@ -256,49 +256,106 @@ static SpecDev to_dev(const fc_spec_state* s) {
   d.T = s->temperature; d.top_k = s->top_k; d.seed = s->seed;
   d.t_len = s->t_len; d.d_len = s->d_len; d.t_pend = s->t_pend; d.d_pend = s->d_pend;
   d.t_pend_n = s->t_pend_n; d.d_pend_n = s->d_pend_n; d.t_dirty = s->t_dirty; d.d_dirty = s->d_dirty;
-  d.gen = s->gen; d.gen_n = s->gen_n; d.prompt_len = s->prompt_len; d.round = s->round; d.result = s->result;
-  d.tok_d0 = s->tok_d0; d.n_d0 = s->n_d0; d.start_d = s->start_d; d.tok_ds = s->tok_ds; d.ones = s->ones;
-  d.tok_v = s->tok_v; d.start_v = s->start_v; d.n_v = s->n_v; d.drafts = s->drafts;
+  d.gen = s->gen; d.gen_n = s->gen_n; d.prompt_len = s->prompt_len; d.round = s->round; d.stall = s->stall;
+  d.result = s->result;
+  d.tok_d0 = s->tok_d0; d.off_d0 = s->off_d0; d.start_d = s->start_d; d.tok_ds = s->tok_ds; d.off_ds = s->off_ds;
+  d.tok_v = s->tok_v; d.off_v = s->off_v; d.start_v = s->start_v; d.drafts = s->drafts;
   d.q_logits = s->q_logits; d.p_logits = s->p_logits; d.q_stats = s->q_stats; d.p_stats = s->p_stats;
   return d;
 }
 
-// Round plan: chunk descriptors for draft step 0 (pending draft tokens,
-// right-aligned in 2 slots), draft steps 1..k-1 and the verify chunk
-// (pending target token + k drafts).
-__global__ void k_spec_plan(SpecDev s, int W0, int Wv) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= s.B) return;
-  const int P = FC_PMAX, K = s.k;
-  // draft step 0: the last dn pending tokens, right-aligned in W0 slots
-  // (dn < d_pend_n only for finished rows, whose state no longer changes)
-  const int dfull = s.d_pend_n[b];
-  const int dn = min(dfull, W0);
-  for (int j = 0; j < W0; ++j) {
-    const int src = j - (W0 - dn) + (dfull - dn);
-    s.tok_d0[b * W0 + j] = src >= dfull - dn ? s.d_pend[b * P + src] : 0;
+__device__ __forceinline__ bool row_finished(const SpecDev& s, int b) {
+  return s.gen_n[b] - s.prompt_len[b] >= s.max_tokens;
+}
+
+// Exclusive scan over the block (blockDim.x == PLAN_THR) of three counts
+// per thread; returns the block totals. `carry` holds the running totals of
+// earlier chunks of rows.
+#define PLAN_THR 1024
+__device__ __forceinline__ void scan3(int v[3], int tot[3], int* sm) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    x[q] = v[q];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x[q], o, WAVE);
+      if (lane >= o) x[q] += y;
+    }
   }
-  s.n_d0[b] = dn;
-  const int dl = s.d_len[b];
-  s.start_d[b] = dl;
-  for (int i = 1; i < K; ++i) s.start_d[i * s.B + b] = dl + dn + i - 1;
-  s.ones[b] = 1;
-  // verify: pending target tokens then the k drafts, right-aligned in Wv slots
-  const int tfull = s.t_pend_n[b];
-  const int tn = min(tfull, Wv - K);
-  for (int j = 0; j < Wv - K; ++j) {
-    const int src = j - (Wv - K - tn) + (tfull - tn);
-    s.tok_v[b * Wv + j] = src >= tfull - tn ? s.t_pend[b * P + src] : 0;
+  __syncthreads();
+  if (lane == 63)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) sm[q * 16 + w] = x[q];
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    int before = 0, all = 0;
+    for (int i = 0; i < PLAN_THR / 64; ++i) {
+      const int t = sm[q * 16 + i];
+      if (i < w) before += t;
+      all += t;
+    }
+    v[q] = before + x[q] - v[q];  // exclusive prefix
+    tot[q] = all;
   }
-  s.start_v[b] = s.t_len[b];
-  s.n_v[b] = tn + K;
+}
+
+// Round plan (one workgroup): packed chunks for draft step 0 (the row's
+// pending draft tokens), draft steps 1..k-1 (one token per active row) and
+// the verify pass (pending target tokens then the k drafts, which the draft
+// samplers write in place). Finished rows and rows waiting for a host
+// catch-up get no tokens.
+__global__ __launch_bounds__(PLAN_THR) void k_spec_plan(SpecDev s) {
+  __shared__ int sm[48];
+  const int P = FC_PMAX, K = s.k, B = s.B;
+  int carry[3] = {0, 0, 0};
+  for (int b0 = 0; b0 < B; b0 += PLAN_THR) {
+    const int b = b0 + threadIdx.x;
+    const bool in = b < B;
+    const bool active = in && !s.stall[b] && !row_finished(s, b);
+    const int dn = active ? s.d_pend_n[b] : 0;
+    const int tn = active ? s.t_pend_n[b] : 0;
+    int v[3] = {dn, active ? 1 : 0, active ? tn + K : 0}, tot[3];
+    scan3(v, tot, sm);
+    if (in) {
+      const int o0 = carry[0] + v[0], o1 = carry[1] + v[1], o2 = carry[2] + v[2];
+      s.off_d0[b] = o0;
+      s.off_ds[b] = o1;
+      s.off_v[b] = o2;
+      for (int j = 0; j < dn; ++j) s.tok_d0[o0 + j] = s.d_pend[b * P + j];
+      for (int j = 0; j < tn; ++j) s.tok_v[o2 + j] = s.t_pend[b * P + j];
+      const int dl = s.d_len[b];
+      s.start_d[b] = dl;
+      for (int i = 1; i < K; ++i) s.start_d[i * B + b] = dl + dn + i - 1;
+      s.start_v[b] = s.t_len[b];
+    }
+#pragma unroll
+    for (int q = 0; q < 3; ++q) carry[q] += tot[q];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    s.off_d0[B] = carry[0];
+    s.off_ds[B] = carry[1];
+    s.off_v[B] = carry[2];
+  }
+}
+
+// Where draft step i's proposal for row b goes: the verify chunk and the
+// next draft step's chunk (active rows only; inactive rows own no slots).
+__device__ __forceinline__ void place_draft(const SpecDev& s, int b, int i, int tok) {
+  s.drafts[b * s.k + i] = tok;
+  const int a0 = s.off_ds[b];
+  if (s.off_ds[b + 1] == a0) return;
+  s.tok_v[s.off_v[b + 1] - s.k + i] = tok;
+  if (i + 1 < s.k) s.tok_ds[(i + 1) * s.B + a0] = tok;
 }
 
 // Draft step i: statistics of the draft logits row, proposal d_{i+1}
 // (flaxchat/engine.py:493-499), written where the next chunks read it.
-__global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i, int Wv) {
+__global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i) {
   __shared__ StatSmem sm;
-  __shared__ int tok_s;
   const int b = blockIdx.x;
   const float* z = s.q_logits + ((int64_t)b * s.k + i) * s.V;
   fc_rowstat* rs = s.q_stats + b * s.k + i;
@@ -307,12 +364,7 @@ __global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i, int Wv)
   const fc_rowstat st = sm.res;
   if (s.T > 0.f) tok = block_draw(z, st, z, st, 0, s.T, s.V, s.seed, b, s.round[b], i, sm);
   else tok = st.argmax;
-  if (threadIdx.x == 0) {
-    tok_s = tok;
-    s.drafts[b * s.k + i] = tok;
-    s.tok_v[b * Wv + (Wv - s.k) + i] = tok;
-    if (i + 1 < s.k) s.tok_ds[(i + 1) * s.B + b] = tok;
-  }
+  if (threadIdx.x == 0) place_draft(s, b, i, tok);
 }
 
 // The rollback state machine after one accept/reject pass: append the
@@ -370,6 +422,7 @@ __device__ void bookkeep(const SpecDev& s, int b, const int* emitted, int n_emit
       s.t_pend[b * P] = gen[gn - 1];
       s.t_pend_n[b] = 1;
       flags |= 1;
+      s.stall[b] = 1;
     }
     if (dp <= P) {
       s.d_len[b] = d_new;
@@ -380,6 +433,7 @@ __device__ void bookkeep(const SpecDev& s, int b, const int* emitted, int n_emit
       s.d_pend[b * P] = gen[gn - 1];
       s.d_pend_n[b] = 1;
       flags |= 2;
+      s.stall[b] = 1;
     }
   }
   if (gn - s.prompt_len[b] >= s.max_tokens) flags |= 4;
@@ -399,7 +453,7 @@ __device__ void bookkeep(const SpecDev& s, int b, const int* emitted, int n_emit
 // drafts, the greedy correction and greedy bonus go to `emitted`; a sampled
 // rejection or bonus is left as a draw request (mode / bonus_draw).
 struct Decision {
-  int mode;        // -1 finished row, 0 no rejection draw, 1 draw from p, 2 from the residual
+  int mode;        // -1 finished, -2 stalled, 0 no rejection draw, 1 draw from p, 2 from the residual
   int row;         // verify row of the rejection draw
   int n, acc, rej, bonus, kp;
   int bonus_draw;  // the bonus token is still to be drawn (sampling)
@@ -407,6 +461,8 @@ struct Decision {
 };
 static_assert(sizeof(Decision) == 32 * sizeof(int), "Decision layout");
 
+// mode -1: the row finished; -2: the row waits for a host catch-up and did
+// nothing this round.
 __device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& d) {
   const int K = s.k, V = s.V;
   const bool greedy = !(s.T > 0.f);
@@ -421,6 +477,11 @@ __device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& 
   d.bonus = 0;
   d.bonus_draw = 0;
   if (kp <= 0) return;
+  if (s.stall[b]) {
+    d.mode = -2;
+    d.kp = 0;
+    return;
+  }
   d.mode = 0;
   int acc = 0, n = 0;
   for (int i = 0; i < kp; ++i) {
@@ -462,11 +523,14 @@ __device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& 
   d.n = n;
 }
 
-__device__ void finished_row(const SpecDev& s, int b) {
+// A finished row (flag 4) or a row waiting for its catch-up (flag 8): no
+// state change; the round counter of a waiting row does not move, so its
+// random stream does not depend on when the host catches it up.
+__device__ void idle_row(const SpecDev& s, int b, int mode) {
   int* res = s.result + (int64_t)b * FC_RES_STRIDE;
-  res[0] = 0; res[1] = 0; res[2] = -1; res[3] = 4; res[4] = 0;
+  res[0] = 0; res[1] = 0; res[2] = -1; res[3] = mode == -2 ? 8 : 4; res[4] = 0;
   res[5] = s.t_pend_n[b]; res[6] = s.d_pend_n[b];
-  s.round[b] += 1;
+  if (mode != -2) s.round[b] += 1;
 }
 
 // Accept/reject with the top-k filter (one workgroup per row): decision,
@@ -479,7 +543,7 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
   if (tid == 0) decide(s, b, s.p_stats + b * (K + 1), d);
   __syncthreads();
   if (d.mode < 0) {
-    if (tid == 0) finished_row(s, b);
+    if (tid == 0) idle_row(s, b, d.mode);
     return;
   }
   const int rnd = s.round[b];
@@ -707,7 +771,7 @@ __device__ __forceinline__ fc_rowstat make_rowstat(const RowMerge& rm, int V) {
 
 // Draft step i without top-k: merge of the step's partials (one wave per row),
 // proposal d_{i+1} written where the next chunks read it.
-__global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, int Wv, const VPart* __restrict__ part,
+__global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, const VPart* __restrict__ part,
                                                          int nch) {
   const int b = blockIdx.x * (VP_THR / 64) + (threadIdx.x >> 6);
   if (b >= s.B) return;
@@ -715,10 +779,7 @@ __global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, int W
   const RowMerge rm = wave_merge_row(part + (int64_t)b * nch, nch, samp, samp);
   if ((threadIdx.x & 63) == 0) {
     s.q_stats[b * s.k + i] = make_rowstat(rm, s.V);
-    const int tok = rm.tok;
-    s.drafts[b * s.k + i] = tok;
-    s.tok_v[b * Wv + (Wv - s.k) + i] = tok;
-    if (i + 1 < s.k) s.tok_ds[(i + 1) * s.B + b] = tok;
+    place_draft(s, b, i, rm.tok);
   }
 }
 
@@ -855,7 +916,7 @@ __global__ __launch_bounds__(64) void k_accept_finish(SpecDev s, const Decision*
   const Decision* d = ctl + b;
   const int mode = d->mode, bonus_draw = d->bonus_draw;
   if (mode < 0) {
-    if (threadIdx.x == 0) finished_row(s, b);
+    if (threadIdx.x == 0) idle_row(s, b, mode);
     return;
   }
   int trej = -1, tbonus = -1;
@@ -904,16 +965,18 @@ static bool chunked(const fc_spec_state* st) {
 
 static int check_spec(const fc_spec_state* st) {
   FC_CHECK_ARG(st && st->batch > 0 && st->k > 0 && st->k <= 16 && st->vocab > 0, "spec state sizes (k in 1..16)");
-  FC_CHECK_ARG(st->t_len && st->d_len && st->gen && st->gen_n && st->result && st->q_logits && st->p_logits &&
-                   st->q_stats && st->p_stats && st->drafts && st->tok_v && st->tok_ds && st->tok_d0 && st->part,
+  FC_CHECK_ARG(st->t_len && st->d_len && st->t_pend && st->d_pend && st->t_pend_n && st->d_pend_n &&
+                   st->t_dirty && st->d_dirty && st->gen && st->gen_n && st->prompt_len && st->round && st->stall &&
+                   st->result && st->q_logits && st->p_logits && st->q_stats && st->p_stats && st->drafts &&
+                   st->tok_v && st->off_v && st->start_v && st->tok_ds && st->off_ds && st->tok_d0 && st->off_d0 &&
+                   st->start_d && st->part,
                "spec state pointers");
   FC_CHECK_ARG(st->part_bytes >= fc_spec_part_bytes(st->batch, st->k, st->vocab),
                "part_bytes below fc_spec_part_bytes(batch, k, vocab)");
   return FC_OK;
 }
 
-extern "C" int32_t fc_spec_accept(const fc_spec_state* st, int32_t w_verify, void* stream) {
-  (void)w_verify;
+extern "C" int32_t fc_spec_accept(const fc_spec_state* st, void* stream) {
   int rc = check_spec(st);
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
@@ -947,9 +1010,55 @@ extern "C" int32_t fc_spec_accept(const fc_spec_state* st, int32_t w_verify, voi
   return FC_OK;
 }
 
+// Chunk capacities of a round (per row: FC_PMAX pending draft tokens at
+// step 0; FC_PMAX pending target tokens + k drafts at verify) and the token
+// counts the kernel shapes are tuned for.
+struct RoundChunks {
+  fc_chunk d0, ds, v;
+};
+static RoundChunks round_chunks(const fc_spec_state* st) {
+  const int B = st->batch, K = st->k, V = st->vocab;
+  RoundChunks r{};
+  r.d0.max_tokens = B * FC_PMAX;
+  r.d0.max_per_row = FC_PMAX;
+  r.d0.typ_tokens = 2 * B;
+  r.d0.tokens = st->tok_d0;
+  r.d0.row_off = st->off_d0;
+  r.d0.start = st->start_d;
+  r.d0.n_out = 1;
+  r.d0.logits = st->q_logits;
+  r.d0.logits_stride = (int64_t)K * V;
+  r.ds = r.d0;
+  r.ds.max_tokens = B;
+  r.ds.max_per_row = 1;
+  r.ds.typ_tokens = B;
+  r.ds.row_off = st->off_ds;
+  r.v.max_tokens = B * (FC_PMAX + K);
+  r.v.max_per_row = FC_PMAX + K;
+  r.v.typ_tokens = B * (K + 2);
+  r.v.tokens = st->tok_v;
+  r.v.row_off = st->off_v;
+  r.v.start = st->start_v;
+  r.v.n_out = K + 1;
+  r.v.logits = st->p_logits;
+  r.v.logits_stride = (int64_t)(K + 1) * V;
+  return r;
+}
+
+extern "C" int64_t fc_spec_workspace_bytes(const fc_model* target, const fc_model* draft, int32_t batch,
+                                           int32_t k) {
+  if (!target || !draft || batch <= 0 || k <= 0 || k > 16) return -1;
+  const int B = batch;
+  int64_t a = fc_forward_workspace_bytes(target, B, B * (FC_PMAX + k), FC_PMAX + k, B * (k + 2));
+  int64_t b = fc_forward_workspace_bytes(draft, B, B * FC_PMAX, FC_PMAX, 2 * B);
+  int64_t c = fc_forward_workspace_bytes(draft, B, B, 1, B);
+  if (a < 0 || b < 0 || c < 0) return -1;
+  return std::max(a, std::max(b, c));
+}
+
 extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache, const fc_model* draft,
-                                 const fc_cache* dcache, const fc_spec_state* st, int32_t w_draft, int32_t w_verify,
-                                 void* work, int64_t work_bytes, void* stream) {
+                                 const fc_cache* dcache, const fc_spec_state* st, void* work, int64_t work_bytes,
+                                 void* stream) {
   int rc = check_spec(st);
   if (rc) return rc;
   FC_CHECK_ARG(target && draft && tcache && dcache, "models / caches");
@@ -958,28 +1067,18 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
   hipStream_t s = (hipStream_t)stream;
   SpecDev d = to_dev(st);
   const int B = st->batch, K = st->k, V = st->vocab;
-  FC_CHECK_ARG(w_draft >= 1 && w_draft <= FC_PMAX, "w_draft must be in [1, FC_PMAX]");
-  FC_CHECK_ARG(w_verify >= K + 1 && w_verify <= FC_PMAX + K, "w_verify must be in [k+1, FC_PMAX+k]");
-  hipLaunchKernelGGL(k_spec_plan, dim3((B + 255) / 256), dim3(256), 0, s, d, w_draft, w_verify);
+  hipLaunchKernelGGL(k_spec_plan, dim3(1), dim3(PLAN_THR), 0, s, d);
   FC_LAUNCH_CHECK();
   const bool fast = chunked(st);
   const PartLayout L = part_layout(st->part, B, K, V);
+  const RoundChunks rcn = round_chunks(st);
   for (int i = 0; i < K; ++i) {
-    fc_chunk ch{};
-    if (i == 0) {
-      ch.W = w_draft;
-      ch.tokens = st->tok_d0;
-      ch.start = st->start_d;
-      ch.nvalid = st->n_d0;
-    } else {
-      ch.W = 1;
+    fc_chunk ch = i == 0 ? rcn.d0 : rcn.ds;
+    if (i > 0) {
       ch.tokens = st->tok_ds + (int64_t)i * B;
       ch.start = st->start_d + (int64_t)i * B;
-      ch.nvalid = st->ones;
     }
-    ch.n_out = 1;
     ch.logits = st->q_logits + (int64_t)i * V;
-    ch.logits_stride = (int64_t)K * V;
     rc = fc_forward(draft, dcache, &ch, work, work_bytes, stream);
     if (rc) return rc;
     if (fast) {
@@ -987,23 +1086,16 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
       rc = launch_vpart(st->q_logits + (int64_t)i * V, (int64_t)K * V, B, V, st->temperature, st->temperature > 0.f,
                         st->seed, st->round, i, L.vp, &nch, s);
       if (rc) return rc;
-      hipLaunchKernelGGL(k_draft_finish, dim3((B + 3) / 4), dim3(VP_THR), 0, s, d, i, w_verify, L.vp, nch);
+      hipLaunchKernelGGL(k_draft_finish, dim3((B + 3) / 4), dim3(VP_THR), 0, s, d, i, L.vp, nch);
     } else {
-      hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i, w_verify);
+      hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i);
     }
     FC_LAUNCH_CHECK();
   }
-  fc_chunk vch{};
-  vch.W = w_verify;
-  vch.tokens = st->tok_v;
-  vch.start = st->start_v;
-  vch.nvalid = st->n_v;
-  vch.n_out = K + 1;
-  vch.logits = st->p_logits;
-  vch.logits_stride = (int64_t)(K + 1) * V;
+  fc_chunk vch = rcn.v;
   rc = fc_forward(target, tcache, &vch, work, work_bytes, stream);
   if (rc) return rc;
-  return fc_spec_accept(st, w_verify, stream);
+  return fc_spec_accept(st, stream);
 }
 
 // ---------------------------------------------------------------------------

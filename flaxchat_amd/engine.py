@@ -29,6 +29,7 @@ from __future__ import annotations
 
 import ctypes
 import weakref
+from collections import deque
 from typing import List, Optional, Sequence, Union
 
 import numpy as np
@@ -36,7 +37,7 @@ import torch
 
 from . import _lib
 from ._lib import FcSpecState, FcRowstat, PMAX, RES_STRIDE, check, lib
-from .runtime import DeviceCache, DeviceModel, Workspace, default_device, forward_chunk, prefill_rows
+from .runtime import DeviceCache, DeviceModel, Workspace, default_device, forward_packed, prefill_rows
 
 _BIG_POS = 0x3FFFFFFF
 _DEVICE_MODELS: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
@@ -87,24 +88,21 @@ def _check_rows(rows, V):
             raise ValueError(f"token id outside [0, {V})")
 
 
-class _Pinned:
-    def __init__(self, like: torch.Tensor):
-        self.h = torch.empty(like.shape, dtype=like.dtype, pin_memory=True)
-
-    def fetch(self, src: torch.Tensor, stream) -> np.ndarray:
-        # the copy must be ordered after the round on the engine's stream
-        with torch.cuda.stream(stream):
-            self.h.copy_(src, non_blocking=True)
-        stream.synchronize()
-        return self.h.numpy()
-
-
 class SpecSession:
-    """Device state of one batched speculative-decoding call."""
+    """Device state of one batched speculative-decoding call.
+
+    Every round has the same launch shapes (chunks are packed and sized for
+    their capacities), so the first eager round is followed by one captured
+    graph that every later round replays. The host keeps `depth` rounds in
+    flight: each round's result record is copied to its own pinned slot, and
+    round r is read while round r + 1 runs. A row whose rollback needs more
+    than FC_PMAX re-fed tokens stalls on the device (it is fed nothing and its
+    round counter does not move) until the host has fed the missing tokens.
+    """
 
     def __init__(self, target: DeviceModel, draft: DeviceModel, rows: List[List[int]], max_tokens: int,
                  temperature: float, top_k: Optional[int], seed: int, draft_steps: int,
-                 use_graph: bool = True, stream: Optional[torch.cuda.Stream] = None):
+                 use_graph: bool = True, stream: Optional[torch.cuda.Stream] = None, depth: int = 2):
         if target.V != draft.V:
             raise VocabMismatchError("Main and draft models must share the same vocabulary size")
         if draft_steps < 1 or draft_steps > 16:
@@ -121,6 +119,7 @@ class SpecSession:
         self.top_k = int(top_k) if top_k is not None and top_k > 0 else 0
         self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
         self.use_graph = use_graph
+        self.depth = max(1, int(depth))
         self.dev = dev = target.device
         self.stream = stream or torch.cuda.Stream(device=dev)
         P = max(len(r) for r in rows)
@@ -139,9 +138,10 @@ class SpecSession:
             self.bufs = dict(
                 t_len=z(B), d_len=z(B), t_pend=z(B, PMAX), d_pend=z(B, PMAX), t_pend_n=z(B), d_pend_n=z(B),
                 t_dirty=torch.full((B,), _BIG_POS, **i32), d_dirty=torch.full((B,), _BIG_POS, **i32),
-                gen=z(B, self.gen_cap), gen_n=z(B), prompt_len=z(B), round=z(B), result=z(B, RES_STRIDE),
-                tok_d0=z(B, PMAX), n_d0=z(B), start_d=z(k, B), tok_ds=z(k, B), ones=torch.ones(B, **i32),
-                tok_v=z(B, PMAX + k), start_v=z(B), n_v=z(B), drafts=z(B, k),
+                gen=z(B, self.gen_cap), gen_n=z(B), prompt_len=z(B), round=z(B), stall=z(B),
+                result=z(B, RES_STRIDE),
+                tok_d0=z(B * PMAX), off_d0=z(B + 1), start_d=z(k, B), tok_ds=z(k, B), off_ds=z(B + 1),
+                tok_v=z(B * (PMAX + k)), off_v=z(B + 1), start_v=z(B), drafts=z(B, k),
                 q_logits=torch.zeros(B, k, V, dtype=torch.float32, device=dev),
                 p_logits=torch.zeros(B, k + 1, V, dtype=torch.float32, device=dev),
                 q_stats=torch.zeros(B * k * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev),
@@ -150,16 +150,16 @@ class SpecSession:
         self.state = FcSpecState(B, k, self.max_tokens, self.gen_cap, V, self.temperature, self.top_k, self.seed,
                                  *[self.bufs[n].data_ptr() for n in _lib._SPEC_PTRS],
                                  self.bufs["part"].data_ptr(), self.bufs["part"].numel())
-        self.ws = Workspace(dev)          # captured by the round graphs: never reallocated after capture
+        self.ws = Workspace(dev)          # captured by the round graph: never reallocated after capture
         self.ws_catchup = Workspace(dev)  # prefill / catch-up
-        nb = max(lib().fc_forward_workspace_bytes(ctypes.byref(m.desc), B, w, w)
-                 for m, w in ((target, PMAX + k), (draft, PMAX)))
+        nb = lib().fc_spec_workspace_bytes(ctypes.byref(target.desc), ctypes.byref(draft.desc), B, k)
+        if nb < 0:
+            raise RuntimeError("fc_spec_workspace_bytes failed")
         with torch.cuda.stream(self.stream):
             self.ws.get(nb)
-        self.graphs = {}                  # (draft chunk width, verify width) -> graph exec
-        self.seen = set()
-        self.w_draft, self.w_verify = 1, k + 1
-        self.res_h = _Pinned(self.bufs["result"])
+        self.graph = None
+        self.launched = 0
+        self.res_h = [torch.empty(B, RES_STRIDE, dtype=torch.int32, pin_memory=True) for _ in range(self.depth)]
         self.rounds = 0
         self.accept_hist = []
 
@@ -176,7 +176,6 @@ class SpecSession:
                 gen[i, :len(r)] = r
             pend = np.zeros((self.B, PMAX), np.int32)
             pend[:, 0] = last
-            dev = self.dev
             b["t_len"].copy_(torch.from_numpy(P - 1))
             b["d_len"].copy_(torch.from_numpy(P - 1))
             b["t_pend"].copy_(torch.from_numpy(pend))
@@ -187,42 +186,39 @@ class SpecSession:
             b["gen_n"].copy_(torch.from_numpy(P))
             b["prompt_len"].copy_(torch.from_numpy(P))
 
-    def _round_call(self, w0, wv):
+    def _round_call(self):
         buf = self.ws.buf
         check(lib().fc_spec_round(ctypes.byref(self.T.desc), ctypes.byref(self.tcache.desc),
                                   ctypes.byref(self.Dm.desc), ctypes.byref(self.dcache.desc),
-                                  ctypes.byref(self.state), w0, wv, buf.data_ptr(), buf.numel(),
+                                  ctypes.byref(self.state), buf.data_ptr(), buf.numel(),
                                   self.stream.cuda_stream), "fc_spec_round")
 
     def launch_round(self):
-        """One round with the current chunk widths: replay its graph, capture
-        it on the second use of these widths, or run it eagerly."""
+        """Enqueue one round: replay the graph, capture it on the second
+        round, or run the first round eagerly."""
         s = self.stream.cuda_stream
-        key = (self.w_draft, self.w_verify)
-        ex = self.graphs.get(key)
-        if ex is not None:
-            check(lib().fc_graph_launch(ex, s), "fc_graph_launch")
-            return
-        if self.use_graph and key in self.seen:
+        if self.graph is not None:
+            check(lib().fc_graph_launch(self.graph, s), "fc_graph_launch")
+        elif self.use_graph and self.launched >= 1:
             check(lib().fc_graph_begin(s), "fc_graph_begin")
             try:
-                self._round_call(*key)
+                self._round_call()
             finally:
                 ex = ctypes.c_void_p()
                 rc = lib().fc_graph_end(s, ctypes.byref(ex))
             check(rc, "fc_graph_end")
-            self.graphs[key] = ex
-            check(lib().fc_graph_launch(ex, s), "fc_graph_launch")
-            return
-        self.seen.add(key)
-        self._round_call(*key)
+            self.graph = ex
+            check(lib().fc_graph_launch(self.graph, s), "fc_graph_launch")
+        else:
+            self._round_call()
+        self.launched += 1
 
     def _catch_up(self, flags):
-        """Rows whose rollback point lies before the last emitted token (after
+        """Rows whose rollback point lies more than FC_PMAX tokens back (after
         a last-index rejection marked the caches stale): feed the missing
-        tokens so each model has exactly one pending token."""
+        tokens so each model has exactly one pending token, then release the
+        row. The caller has drained the stream."""
         b = self.bufs
-        self.stream.synchronize()
         gen = b["gen"].cpu().numpy()
         gen_n = b["gen_n"].cpu().numpy()
         for bit, dm, cache, key in ((1, self.T, self.tcache, "t_len"), (2, self.Dm, self.dcache, "d_len")):
@@ -242,31 +238,55 @@ class SpecSession:
                 prefill_rows(dm, cache, rows, starts, self.ws_catchup)
                 new = np.where(sel, gen_n - 1, lens).astype(np.int32)
                 b[key].copy_(torch.from_numpy(new))
+        with torch.cuda.stream(self.stream):
+            st = b["stall"].cpu().numpy()
+            st[(flags & 3) != 0] = 0
+            b["stall"].copy_(torch.from_numpy(st))
+
+    def _record(self, res) -> int:
+        active = res[:, 4] > 0
+        if active.any():
+            self.rounds += 1
+            self.accept_hist.append(res[active, 1].copy())
+        return int(np.bitwise_or.reduce(res[:, 3]))
 
     def run(self, max_rounds: Optional[int] = None):
+        """Run rounds until every row has max_tokens (or max_rounds rounds)."""
+        inflight = deque()
         n = 0
+        stop = False
         while True:
-            with torch.cuda.stream(self.stream):
-                self.launch_round()
-            res = self.res_h.fetch(self.bufs["result"], self.stream)
-            self.rounds += 1
-            n += 1
+            while not stop and len(inflight) < self.depth:
+                slot = self.launched % self.depth
+                with torch.cuda.stream(self.stream):
+                    self.launch_round()
+                    self.res_h[slot].copy_(self.bufs["result"], non_blocking=True)
+                    ev = torch.cuda.Event()
+                    ev.record(self.stream)
+                inflight.append((ev, slot))
+                n += 1
+                if max_rounds is not None and n >= max_rounds:
+                    stop = True
+            if not inflight:
+                break
+            ev, slot = inflight.popleft()
+            ev.synchronize()
+            res = self.res_h[slot].numpy().copy()
+            self._record(res)
             flags = res[:, 3]
-            active = res[:, 4] > 0
-            if active.any():
-                self.accept_hist.append(res[active, 1].copy())
             if (flags & 3).any():
+                flags = flags.copy()
+                while inflight:  # later rounds left the stalled rows alone; other rows may stall too
+                    ev2, slot2 = inflight.popleft()
+                    ev2.synchronize()
+                    res2 = self.res_h[slot2].numpy().copy()
+                    self._record(res2)
+                    flags |= res2[:, 3] & 3
+                self.stream.synchronize()
                 self._catch_up(flags)
-            live = (flags & 4) == 0
-            if live.any():
-                t_pend = np.where(flags & 1, 1, res[:, 5])[live]
-                d_pend = np.where(flags & 2, 1, res[:, 6])[live]
-                self.w_draft = int(max(1, d_pend.max()))
-                self.w_verify = int(t_pend.max()) + self.k
-            if (flags & 4).all():
-                break
-            if max_rounds is not None and n >= max_rounds:
-                break
+                continue
+            if ((flags & 4) != 0).all():
+                stop = True
 
     def outputs(self) -> List[List[int]]:
         self.stream.synchronize()
@@ -280,9 +300,9 @@ class SpecSession:
         return int(np.minimum(gen_n - P, self.max_tokens).sum())
 
     def close(self):
-        for ex in self.graphs.values():
-            lib().fc_graph_destroy(ex)
-        self.graphs = {}
+        if self.graph is not None:
+            lib().fc_graph_destroy(self.graph)
+            self.graph = None
 
     def __del__(self):
         try:
@@ -343,13 +363,13 @@ class FastSession:
             self.done = torch.zeros(B, **i32)
             self.step = torch.zeros(B, **i32)
             self.max_pos = torch.zeros(B, **i32)
-            self.tok = torch.zeros(B, 1, **i32)
-            self.ones = torch.ones(B, **i32)
+            self.tok = torch.zeros(B, **i32)
+            self.row_off = torch.arange(B + 1, **i32)
             self.logits = torch.zeros(B, dm.V, dtype=torch.float32, device=dev)
             self.stats = torch.zeros(B * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev)
         self.ws = Workspace(dev)
         self.ws_pre = Workspace(dev)
-        nb = lib().fc_forward_workspace_bytes(ctypes.byref(dm.desc), B, 1, 1)
+        nb = lib().fc_forward_workspace_bytes(ctypes.byref(dm.desc), B, B, 1, B)
         with torch.cuda.stream(self.stream):
             self.ws.get(nb)
         self.graph = None
@@ -364,12 +384,12 @@ class FastSession:
                 gen[i, :len(r)] = r
             self.gen.copy_(torch.from_numpy(gen))
             self.pos.copy_(torch.from_numpy(P - 1))
-            self.tok.copy_(torch.from_numpy(np.array([r[-1] for r in self.rows], np.int32)[:, None]))
+            self.tok.copy_(torch.from_numpy(np.array([r[-1] for r in self.rows], np.int32)))
             self.max_pos.copy_(torch.from_numpy(P + self.max_tokens - 1))
 
     def _step_call(self):
         s = self.stream.cuda_stream
-        forward_chunk(self.dm, self.cache, self.tok, self.pos, self.ones, 1, self.logits, self.ws, s)
+        forward_packed(self.dm, self.cache, self.tok, self.row_off, self.pos, 1, 1, self.logits, self.ws, s)
         check(lib().fc_fast_sample(self.logits.data_ptr(), self.B, self.dm.V, self.temperature, self.top_k,
                                    self.seed, self.eos, self.gen.data_ptr(), self.cap, self.pos.data_ptr(),
                                    self.done.data_ptr(), self.step.data_ptr(), self.max_pos.data_ptr(),

@@ -33,15 +33,49 @@ def _ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+def frag_pack(a: np.ndarray) -> np.ndarray:
+    """Fragment order (include/flaxchat_amd.h) of a [R][K] matrix as a
+    [round16(R)][K] array whose memory is in fragment order (zero padding)."""
+    R, K = a.shape
+    assert K % 32 == 0, "fragment order needs K % 32 == 0"
+    R16 = (R + 15) // 16 * 16
+    pad = np.zeros((R16, K), a.dtype)
+    pad[:R] = a
+    return np.ascontiguousarray(pad.reshape(R16 // 16, 16, K // 32, 4, 8).transpose(0, 2, 3, 1, 4)).reshape(R16, K)
+
+
+def frag_unpack(p: np.ndarray, R: int) -> np.ndarray:
+    """Inverse of frag_pack: the first R rows of the row-major matrix."""
+    R16, K = p.shape
+    return np.ascontiguousarray(p.reshape(R16 // 16, K // 32, 4, 16, 8).transpose(0, 3, 1, 2, 4)).reshape(R16, K)[:R]
+
+
+def pack_operand(t: torch.Tensor) -> torch.Tensor:
+    """Device copy of a row-major bf16 [R][K] matrix in fragment order
+    ([round16(R)][K]), through fc_pack_operand on the current stream."""
+    R, K = t.shape
+    if K % 64 != 0 or R % 32 != 0:
+        raise ValueError(f"bf16 weights need rows % 32 == 0 and K % 64 == 0 (got {R} x {K})")
+    out = torch.empty(((R + 15) // 16 * 16, K), dtype=t.dtype, device=t.device)
+    check(lib().fc_pack_operand(t.data_ptr(), out.data_ptr(), R, K, torch.cuda.current_stream().cuda_stream),
+          "fc_pack_operand")
+    return out
+
+
 def default_device() -> torch.device:
     if not torch.cuda.is_available():
         raise RuntimeError("flaxchat_amd needs a ROCm GPU (torch.cuda.is_available() is False)")
     return torch.device("cuda", torch.cuda.current_device())
 
 
+_MATS = ("wqkv", "wo", "wfc", "wproj")
+
+
 class DeviceModel:
     """A model's parameters in the engine's HBM layout plus the fc_model
-    descriptor the kernels read (include/flaxchat_amd.h: fc_model/fc_layer)."""
+    descriptor the kernels read (include/flaxchat_amd.h: fc_model/fc_layer).
+    In bf16 the linear weights and lm_head are in fragment order; wte and
+    the value-embedding tables stay row-major (they are gathered by token)."""
 
     def __init__(self, config: GPTConfig, dtype: int, device, tensors: dict, scalars: dict):
         self.config = config
@@ -89,18 +123,25 @@ class DeviceModel:
         def up(a, dt=tdt):
             return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device=device, dtype=dt)
 
+        def mat(a):  # a linear weight [out][in] in the GEMM layout of this dtype
+            t = up(a)
+            return pack_operand(t) if code == _lib.FC_BF16 else t
+
         layers = []
         for i, blk in enumerate(model.blocks):
             a = blk.attn
             wqkv = np.concatenate([a.c_q.kernel.T, a.c_k.kernel.T, a.c_v.kernel.T], axis=0)
-            lt = dict(wqkv=up(wqkv), wo=up(a.c_proj.kernel.T), wfc=up(blk.mlp.c_fc.kernel.T),
-                      wproj=up(blk.mlp.c_proj.kernel.T))
+            lt = dict(wqkv=mat(wqkv), wo=mat(a.c_proj.kernel.T), wfc=mat(blk.mlp.c_fc.kernel.T),
+                      wproj=mat(blk.mlp.c_proj.kernel.T))
             if str(i) in model.value_embeds:
                 lt["ve"] = up(model.value_embeds[str(i)].embedding)
                 lt["ve_gate"] = up(a.ve_gate.kernel.T, torch.float32)
             layers.append(lt)
         wte = up(model.wte.embedding)
-        lm = wte if model._tie_embeddings else up(model.lm_head.kernel.T)
+        if code == _lib.FC_BF16:
+            lm = pack_operand(wte) if model._tie_embeddings else mat(model.lm_head.kernel.T)
+        else:
+            lm = wte if model._tie_embeddings else up(model.lm_head.kernel.T)
         cos, sin = cls._rope(c, device)
         tensors = dict(wte=wte, lm_head=lm, layers=layers, rope_cos=cos, rope_sin=sin,
                        smear_gate=up(model.smear_gate.kernel.reshape(-1), torch.float32))
@@ -134,11 +175,20 @@ class DeviceModel:
                 flat[s:s + n] = (torch.randn(n, device=device, generator=gen) * std).to(dt)
             return out
 
+        bf16 = code == _lib.FC_BF16
+
+        def mat(*shape):
+            t = nrm(*shape)
+            return pack_operand(t) if bf16 else t
+
         wte = nrm(Vp, D)
-        lm = wte if c.tie_embeddings else nrm(Vp, D)
+        if c.tie_embeddings:
+            lm = pack_operand(wte) if bf16 else wte
+        else:
+            lm = mat(Vp, D)
         layers = []
         for i in range(L):
-            lt = dict(wqkv=nrm((H + 2 * G) * d, D), wo=nrm(D, D), wfc=nrm(4 * D, D), wproj=nrm(D, 4 * D))
+            lt = dict(wqkv=mat((H + 2 * G) * d, D), wo=mat(D, D), wfc=mat(4 * D, D), wproj=mat(D, 4 * D))
             if has_ve(i, L):
                 lt["ve_gate"] = nrm(G, 12, dt=torch.float32)
             layers.append(lt)
@@ -217,46 +267,58 @@ class Workspace:
         return self.buf
 
 
-def forward_chunk(dm: DeviceModel, cache: DeviceCache, tokens: torch.Tensor, start: torch.Tensor,
-                  nvalid: torch.Tensor, n_out: int, logits: Optional[torch.Tensor], ws: Workspace,
-                  stream=None, logits_stride: Optional[int] = None):
-    """Feed tokens[B][W] (valid slots right-aligned) at positions start[b]..;
-    write softcapped logits of the last n_out slots into logits[B][n_out][V]."""
-    B, W = tokens.shape
-    assert B == cache.batch and tokens.dtype == torch.int32
-    nbytes = lib().fc_forward_workspace_bytes(ctypes.byref(dm.desc), B, W, n_out)
+def forward_packed(dm: DeviceModel, cache: DeviceCache, tokens: torch.Tensor, row_off: torch.Tensor,
+                   start: torch.Tensor, max_per_row: int, n_out: int, logits: Optional[torch.Tensor],
+                   ws: Workspace, stream=None, logits_stride: Optional[int] = None, typ_tokens: int = 0):
+    """Feed a packed chunk (include/flaxchat_amd.h, fc_chunk): row b's tokens
+    are tokens[row_off[b]:row_off[b+1]] at positions start[b].. (device int32
+    arrays; tokens has the chunk's capacity). Writes softcapped logits of the
+    last n_out tokens of each row into logits[B][n_out][V]."""
+    B = cache.batch
+    max_tokens = int(tokens.numel())
+    assert tokens.dtype == torch.int32 and row_off.numel() == B + 1 and start.numel() == B
+    nbytes = lib().fc_forward_workspace_bytes(ctypes.byref(dm.desc), B, max_tokens, max_per_row, typ_tokens)
     if nbytes < 0:
         raise RuntimeError("fc_forward_workspace_bytes failed")
     buf = ws.get(nbytes)
     stride = logits_stride if logits_stride is not None else n_out * dm.V
-    ch = FcChunk(W, tokens.data_ptr(), start.data_ptr(), nvalid.data_ptr(), n_out,
-                 _ptr(logits) if n_out > 0 else 0, stride)
+    ch = FcChunk(max_tokens, max_per_row, typ_tokens, tokens.data_ptr(), row_off.data_ptr(), start.data_ptr(),
+                 n_out, _ptr(logits) if n_out > 0 else 0, stride)
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
     check(lib().fc_forward(ctypes.byref(dm.desc), ctypes.byref(cache.desc), ctypes.byref(ch),
                            buf.data_ptr(), buf.numel(), s), "fc_forward")
 
 
+def pack_rows(rows: List[List[int]]):
+    """(tokens, row_off, max_per_row) of host token lists in the packed layout."""
+    n = np.array([len(r) for r in rows], np.int64)
+    off = np.zeros(len(rows) + 1, np.int32)
+    off[1:] = np.cumsum(n)
+    tok = np.zeros(max(1, int(off[-1])), np.int32)
+    for b, r in enumerate(rows):
+        tok[off[b]:off[b + 1]] = r
+    return tok, off, max(1, int(n.max()) if len(rows) else 1)
+
+
+def forward_rows(dm: DeviceModel, cache: DeviceCache, rows: List[List[int]], starts: List[int], n_out: int,
+                 logits: Optional[torch.Tensor], ws: Workspace, stream=None):
+    """Feed host token lists rows[b] at positions starts[b].. in one chunk."""
+    dev = dm.device
+    tok, off, mpr = pack_rows(rows)
+    forward_packed(dm, cache, torch.from_numpy(tok).to(dev), torch.from_numpy(off).to(dev),
+                   torch.from_numpy(np.asarray(starts, np.int32)).to(dev), mpr, n_out, logits, ws, stream)
+
+
 def prefill_rows(dm: DeviceModel, cache: DeviceCache, rows: List[List[int]], starts: List[int], ws: Workspace,
                  chunk: int = 256, stream=None):
-    """Feed rows[b] at positions starts[b].. (no logits), in chunks of `chunk`
-    slots; rows may have different lengths (empty rows are skipped)."""
-    B = cache.batch
-    dev = dm.device
+    """Feed rows[b] at positions starts[b].. (no logits), in chunks of up to
+    `chunk` tokens per row; rows may have different lengths (a row with
+    nothing left feeds nothing)."""
     n_max = max((len(r) for r in rows), default=0)
     for c0 in range(0, n_max, chunk):
-        W = min(chunk, n_max - c0)
-        tok = np.zeros((B, W), np.int32)
-        st = np.zeros(B, np.int32)
-        nv = np.zeros(B, np.int32)
-        for b, r in enumerate(rows):
-            piece = r[c0:c0 + W]
-            n = len(piece)
-            if n:
-                tok[b, W - n:] = piece
-            st[b] = starts[b] + c0
-            nv[b] = n
-        forward_chunk(dm, cache, torch.from_numpy(tok).to(dev), torch.from_numpy(st).to(dev),
-                      torch.from_numpy(nv).to(dev), 0, None, ws, stream)
+        pieces = [r[c0:c0 + chunk] for r in rows]
+        st = [starts[b] + c0 for b in range(len(rows))]
+        forward_rows(dm, cache, pieces, st, 0, None, ws, stream)
 
 
 def to_host(dm: DeviceModel):
@@ -264,11 +326,14 @@ def to_host(dm: DeviceModel):
     (in, out) kernel orientation). Shared tensors stay shared."""
     from .gpt import GPT, Attention, Block, Embed, Linear, MLP
     memo = {}
+    packed = dm.dtype == _lib.FC_BF16
 
-    def get(t, transpose=False):
-        key = (t.data_ptr(), transpose)
+    def get(t, transpose=False, frag=False):
+        key = (t.data_ptr(), transpose, frag)
         if key not in memo:
             a = t.float().cpu().numpy()
+            if frag and packed:
+                a = frag_unpack(a, a.shape[0])
             memo[key] = a.T if transpose else a
         return memo[key]
 
@@ -276,15 +341,15 @@ def to_host(dm: DeviceModel):
     H, G, d = dm.H, dm.G, dm.hd
     blocks, ves = [], {}
     for i, lt in enumerate(dm.t["layers"]):
-        wqkv = get(lt["wqkv"])
+        wqkv = get(lt["wqkv"], frag=True)
         attn = Attention(Linear(wqkv[:H * d].T), Linear(wqkv[H * d:(H + G) * d].T), Linear(wqkv[(H + G) * d:].T),
-                         Linear(get(lt["wo"], True)))
+                         Linear(get(lt["wo"], True, True)))
         if "ve" in lt:
             attn.ve_gate = Linear(get(lt["ve_gate"], True))
             ves[str(i)] = Embed(get(lt["ve"]))
-        blocks.append(Block(attn, MLP(Linear(get(lt["wfc"], True)), Linear(get(lt["wproj"], True)))))
+        blocks.append(Block(attn, MLP(Linear(get(lt["wfc"], True, True)), Linear(get(lt["wproj"], True, True)))))
     wte = Embed(get(dm.t["wte"]))
-    lm = None if c.tie_embeddings else Linear(get(dm.t["lm_head"], True))
+    lm = None if c.tie_embeddings else Linear(get(dm.t["lm_head"], True, True))
     return GPT(c, wte, blocks, lm, np.array(dm.s["resid"], np.float32), np.array(dm.s["x0"], np.float32),
                Linear(get(dm.t["smear_gate"]).reshape(24, 1)), np.float32(dm.s["smear_lambda"]),
                np.float32(dm.s["backout_lambda"]), ves)

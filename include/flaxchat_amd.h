@@ -13,16 +13,23 @@
  * (flaxchat_amd/engine.py) keeps the reference's call surface,
  * generate_speculative() and generate_fast(), on top of this ABI.
  *
- * Layouts (row-major, C order):
- *   Linear weights   [out][in]   (the transpose of Flax's (in, out) kernel)
+ * Layouts (row-major, C order, unless noted):
+ *   Linear weights   [out][in]   (the transpose of Flax's (in, out) kernel); in
+ *                    bf16 stored in fragment order (below), in fp32 row-major
+ *   fragment order   of a bf16 matrix-core operand [R][K] (R padded to a
+ *                    multiple of 16, K % 32 == 0): 16-row x 32-k blocks of
+ *                    1 KB in [row block][k step] order; byte 16*l of a block
+ *                    holds row l % 16, k = 8*(l/16) .. +7 of the step.
+ *                    fc_pack_operand converts a row-major matrix.
  *   K cache          [layer][batch][kv_head][cap][head_dim]
  *   V cache          [layer][batch][kv_head][cap/32][head_dim][32]
  *                    (32-position blocks stored transposed so that the
  *                    P·V matrix-core operand is one 16-byte load per lane)
  *   smear history    [batch][cap][n_embd] fp32 (smeared embedding per position)
- *   chunk tokens     [batch][W], valid slots right-aligned: slot j of row b
- *                    is valid iff j >= W - nvalid[b]; its position is
- *                    start[b] + j - (W - nvalid[b]).
+ *   chunk tokens     packed: row b feeds tokens[row_off[b]] .. tokens[row_off[b+1]-1]
+ *                    at positions start[b], start[b]+1, ...; row_off[batch] is the
+ *                    chunk's total, a device value (rows may feed nothing).
+ *                    Per-token activations (q, y) are packed the same way.
  */
 #ifndef FLAXCHAT_AMD_H
 #define FLAXCHAT_AMD_H
@@ -76,14 +83,19 @@ typedef struct fc_cache {
   int32_t batch, cap;     /* cap is a multiple of 32                          */
 } fc_cache;
 
-/* One chunk of tokens per row, fed at per-row positions. */
+/* One chunk of tokens per row, fed at per-row positions (packed layout
+ * above). The capacities size the grids and the workspace; kernel shapes
+ * are tuned for typ_tokens. */
 typedef struct fc_chunk {
-  int32_t W;
-  const int32_t* tokens;  /* [B][W]  device                                   */
-  const int32_t* start;   /* [B]     device                                   */
-  const int32_t* nvalid;  /* [B]     device                                   */
-  int32_t n_out;          /* logits for the last n_out slots of each row      */
-  float* logits;          /* row (b, r) at logits + b*logits_stride + r*V     */
+  int32_t max_tokens;     /* capacity: row_off[batch] <= max_tokens           */
+  int32_t max_per_row;    /* no row feeds more tokens (<= 1024)               */
+  int32_t typ_tokens;     /* typical total (0: max_tokens)                    */
+  const int32_t* tokens;  /* [max_tokens]  device, packed                     */
+  const int32_t* row_off; /* [batch+1]     device, row_off[0] == 0            */
+  const int32_t* start;   /* [batch]       device, position of the first token */
+  int32_t n_out;          /* logits for the last n_out tokens of each row     */
+  float* logits;          /* row (b, r) at logits + b*logits_stride + r*V;    */
+                          /* unspecified for a row with fewer than n_out tokens */
   int64_t logits_stride;  /* floats between rows b and b+1                    */
 } fc_chunk;
 
@@ -112,16 +124,18 @@ typedef struct fc_spec_state {
   int32_t* gen;    int32_t* gen_n;       /* [B][gen_cap] tokens incl. prompt   */
   int32_t* prompt_len;                   /* [B]                                */
   int32_t* round;                        /* [B] round counter (Philox)         */
+  int32_t* stall;                        /* [B] nonzero: row waits for the host */
+                                         /* catch-up (more than FC_PMAX pending) */
   int32_t* result;                       /* [B][FC_RES_STRIDE]                 */
-  /* per-round scratch */
-  int32_t* tok_d0;   /* [B][FC_PMAX]    draft chunk 0 tokens                   */
-  int32_t* n_d0;     /* [B]                                                    */
+  /* per-round scratch (chunks in the packed layout) */
+  int32_t* tok_d0;   /* [B*FC_PMAX]     draft step 0 tokens                    */
+  int32_t* off_d0;   /* [B+1]                                                  */
   int32_t* start_d;  /* [k][B]          draft step start positions             */
   int32_t* tok_ds;   /* [k][B]          draft step tokens (steps 1..k-1)       */
-  int32_t* ones;     /* [B]             all 1                                  */
-  int32_t* tok_v;    /* [B][FC_PMAX+k]  verify chunk tokens                    */
+  int32_t* off_ds;   /* [B+1]           rows fed at steps 1..k-1               */
+  int32_t* tok_v;    /* [B*(FC_PMAX+k)] verify chunk tokens                    */
+  int32_t* off_v;    /* [B+1]                                                  */
   int32_t* start_v;  /* [B]                                                    */
-  int32_t* n_v;      /* [B]                                                    */
   int32_t* drafts;   /* [B][k]                                                 */
   float* q_logits;   /* [B][k][V]                                              */
   float* p_logits;   /* [B][k+1][V]                                            */
@@ -137,15 +151,18 @@ typedef struct fc_spec_state {
  * normally 1 (target) or 1-2 (draft); after a rejection that rolls back past
  * a stale cache entry, up to FC_PMAX. Result row layout: [0] n_emitted this
  * round, [1] accepted, [2] rejected index or -1, [3] flags (bit0 target
- * needs catch-up, bit1 draft needs catch-up: more than FC_PMAX pending; bit2
- * row finished), [4] k', [5] target pending count, [6] draft pending count,
+ * needs catch-up, bit1 draft needs catch-up: more than FC_PMAX pending, the
+ * row then stalls until the host feeds the missing tokens and clears
+ * stall[b]; bit2 row finished; bit3 row stalled this round, nothing done),
+ * [4] k', [5] target pending count, [6] draft pending count,
  * [8..8+k+1] emitted tokens. */
 
 const char* fc_last_error(void);
 int32_t fc_version(void);
 
-/* Bytes of workspace fc_forward needs for `batch` rows of W slots. */
-int64_t fc_forward_workspace_bytes(const fc_model* m, int32_t batch, int32_t W, int32_t n_out);
+/* Bytes of workspace fc_forward needs for chunks with these capacities. */
+int64_t fc_forward_workspace_bytes(const fc_model* m, int32_t batch, int32_t max_tokens,
+                                   int32_t max_per_row, int32_t typ_tokens);
 
 /* Feed one chunk through the model: embedding + smear, every block, head.
  * Replaces the per-token `_single_step_forward` (flaxchat/engine.py:51-177)
@@ -158,19 +175,28 @@ int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chunk* ch,
  * `dtype`. Replaces the nnx.Linear matmuls of flaxchat/engine.py:106-108,
  * 158, 161, 172 (flaxchat/gpt.py:93-99, 154-163). epi: 0 store fp32,
  * 1 add into fp32 out, 2 relu^2 (flaxchat/gpt.py:161) stored in `dtype`,
- * 4 15*tanh(z/15) softcap (flaxchat/engine.py:173-174) stored fp32. */
+ * 4 15*tanh(z/15) softcap (flaxchat/engine.py:173-174) stored fp32.
+ * bf16: A, W and a bf16 relu^2 output are in fragment order (A padded to
+ * round16(M) rows), K % 64 == 0, N % 32 == 0; fp32: all row-major. */
 int32_t fc_gemm(const void* A, const void* W, void* out, int32_t M, int32_t N, int32_t K,
                 int32_t dtype, int32_t epi, void* stream);
 
+/* Fragment-order copy of a row-major bf16 matrix src[rows][K] into
+ * dst[round16(rows)][K] (padding rows zero). No reference counterpart: the
+ * layout change of the bf16 weights and GEMM operands. */
+int32_t fc_pack_operand(const void* src, void* dst, int32_t rows, int32_t K, void* stream);
+
 /* Split-KV flash-decode attention over a cache layer (flaxchat/engine.py:128-156):
  * GQA head grouping, causal + inclusive sliding window `pos - j <= window`.
- * q: [B][W][H][hd] dtype; y: [B][W][H*hd] dtype. */
-int64_t fc_attention_workspace_bytes(int32_t batch, int32_t W, int32_t n_head, int32_t n_kv_head,
+ * q: [tokens][H][hd] dtype, packed (row_off, start as in fc_chunk);
+ * y: [tokens][H*hd] dtype (rows past row_off[batch] untouched). */
+int64_t fc_attention_workspace_bytes(int32_t batch, int32_t max_per_row, int32_t n_head, int32_t n_kv_head,
                                      int32_t head_dim, int32_t max_keys);
 int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y,
-                     int32_t batch, int32_t W, int32_t n_head, int32_t n_kv_head, int32_t head_dim,
-                     int32_t cap, const int32_t* start, const int32_t* nvalid, int32_t window,
-                     int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes, void* stream);
+                     int32_t batch, int32_t max_per_row, int32_t n_head, int32_t n_kv_head,
+                     int32_t head_dim, int32_t cap, const int32_t* row_off, const int32_t* start,
+                     int32_t window, int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes,
+                     void* stream);
 
 /* Per-row statistics of fp32 logits rows (flaxchat/engine.py:461-476):
  * lax.top_k keep-set (exactly k, lower index first among ties), max and
@@ -179,15 +205,14 @@ int32_t fc_row_stats(const float* logits, int32_t rows, int32_t V, float tempera
                      int32_t top_k, fc_rowstat* stats, void* stream);
 
 /* One speculative round on device (flaxchat/engine.py:484-606 with the
- * sequential verify replaced by one (k+1)-token verify chunk and the
- * re-prefill replaced by length-pointer rollback): draft k steps,
- * verify, accept/reject with residual resampling, bonus, bookkeeping. */
+ * sequential verify replaced by one (pending + k)-token verify chunk and the
+ * re-prefill replaced by length-pointer rollback): draft k steps, verify,
+ * accept/reject with residual resampling, bonus, bookkeeping. Every launch
+ * shape is fixed by (batch, k), so one captured graph replays every round. */
+int64_t fc_spec_workspace_bytes(const fc_model* target, const fc_model* draft, int32_t batch, int32_t k);
 int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
                       const fc_model* draft, const fc_cache* dcache,
-                      const fc_spec_state* st, int32_t w_draft, int32_t w_verify,
-                      void* work, int64_t work_bytes, void* stream);
-/* w_draft >= every active row's draft pending count (chunk width of draft
- * step 0); w_verify >= every active row's target pending count + k. */
+                      const fc_spec_state* st, void* work, int64_t work_bytes, void* stream);
 
 /* Bytes of fc_spec_state.part: per-chunk partials of the vocab-wide passes
  * (row statistics and Gumbel-max draws split over many workgroups). */
@@ -195,7 +220,7 @@ int64_t fc_spec_part_bytes(int32_t batch, int32_t k, int32_t vocab);
 
 /* Accept/reject step alone on given logits (flaxchat/engine.py:525-592);
  * updates the state like fc_spec_round does. */
-int32_t fc_spec_accept(const fc_spec_state* st, int32_t w_verify, void* stream);
+int32_t fc_spec_accept(const fc_spec_state* st, void* stream);
 
 /* generate_fast sampling step (flaxchat/engine.py:308-324, 343-368): for
  * rows with !done[b] && pos[b] < max_pos[b], sample from logits row b,

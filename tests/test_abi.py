@@ -44,7 +44,7 @@ def test_argument_errors_are_status_codes():
     rc = L.fc_attention(None, None, None, None, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None, 0, None)
     assert rc == -1
     st = _lib.FcSpecState()
-    assert L.fc_spec_accept(ctypes.byref(st), 5, None) == -1
+    assert L.fc_spec_accept(ctypes.byref(st), None) == -1
 
 
 def test_struct_layout_matches_c(tmp_path):
@@ -77,6 +77,6 @@ def test_workspace_size_query_needs_no_gpu():
     m.n_layer, m.n_embd, m.n_head, m.n_kv_head, m.head_dim = 2, 256, 2, 2, 128
     m.vocab = m.vocab_pad = 8192
     m.dtype = 1
-    nb = _lib.lib().fc_forward_workspace_bytes(ctypes.byref(m), 4, 5, 5)
-    assert nb > 4 * 5 * 256 * 4 * 3
+    nb = _lib.lib().fc_forward_workspace_bytes(ctypes.byref(m), 4, 20, 5, 0)
+    assert nb > 20 * 256 * 4 * 3
     assert _lib.lib().fc_attention_workspace_bytes(4, 5, 6, 6, 128, 1024) > 0

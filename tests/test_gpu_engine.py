@@ -17,7 +17,7 @@ torch = pytest.importorskip("torch")
 from flaxchat_amd import _lib  # noqa: E402
 from flaxchat_amd.engine import (SpecSession, generate_fast, generate_speculative,  # noqa: E402
                                  generate_with_cache, as_device_model, VocabMismatchError)
-from flaxchat_amd.runtime import DeviceCache, DeviceModel, Workspace, forward_chunk  # noqa: E402
+from flaxchat_amd.runtime import DeviceCache, DeviceModel, Workspace, forward_rows  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -42,10 +42,8 @@ def _device_logits(model, tokens, dtype, chunks):
     out = []
     pos = 0
     for w in chunks:
-        tok = torch.tensor([tokens[pos:pos + w]], dtype=torch.int32, device=dm.device)
         lg = torch.zeros(1, w, dm.V, device=dm.device)
-        forward_chunk(dm, cache, tok, torch.tensor([pos], dtype=torch.int32, device=dm.device),
-                      torch.tensor([w], dtype=torch.int32, device=dm.device), w, lg, ws)
+        forward_rows(dm, cache, [tokens[pos:pos + w]], [pos], w, lg, ws)
         out.append(lg[0].cpu().numpy())
         pos += w
     torch.cuda.synchronize()

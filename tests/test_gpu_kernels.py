@@ -39,31 +39,45 @@ def bf(x):
 
 
 # ---------------------------------------------------------------- GEMM
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
-@pytest.mark.parametrize("M", [1, 3, 5, 16, 32, 64, 100, 224, 300])
-@pytest.mark.parametrize("epi", [0, 1, 2, 4])
-@pytest.mark.parametrize("NK", [(256, 384), (1536, 6144)])
+def _gemm_cases():
+    """Small shapes for every (dtype, M, epilogue); model-sized shapes for the
+    kernel paths they add (split tiles, 6144-deep K) without repeating the
+    epilogue checks."""
+    cases = []
+    for NK in [(256, 384), (1536, 6144)]:
+        for M in [1, 3, 5, 16, 32, 64, 100, 224, 300]:
+            for epi in [0, 1, 2, 4]:
+                for dtype in ["fp32", "bf16"]:
+                    big = NK[0] * NK[1] > 1e6
+                    if big and (epi in (1, 4) or (dtype == "fp32" and M > 64)):
+                        continue
+                    cases.append((dtype, M, epi, NK))
+    return cases
+
+
+@pytest.mark.parametrize("dtype,M,epi,NK", _gemm_cases())
 def test_gemm_parity(dtype, M, epi, NK):
-    """Small and model-sized shapes through every kernel family (VALU GEMV,
-    streaming MFMA, LDS-tiled MFMA with 64-row and full-M tiles)."""
+    """Every kernel family (VALU GEMV in fp32; matrix-core tiles of 16, 32 and
+    64 rows on fragment-order operands in bf16) against float64."""
+    from flaxchat_amd.runtime import frag_pack, frag_unpack
     _say(f"gemm dtype={dtype} M={M} epi={epi} NK={NK}")
     rng = np.random.default_rng(M * 10 + epi)
     N, K = NK
-    if N * K > 1e6 and (epi in (1, 4) or (dtype == "fp32" and M > 64)):
-        pytest.skip("covered by the small shape; keeps the run short")
     A = rng.standard_normal((M, K)).astype(np.float32)
     W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
     if dtype == "bf16":
         A, W = bf(A), bf(W)
         tdt, code = torch.bfloat16, _lib.FC_BF16
+        A_dev, W_dev = frag_pack(A), frag_pack(W)
     else:
         tdt, code = torch.float32, _lib.FC_F32
+        A_dev, W_dev = A, W
     ref = A.astype(np.float64) @ W.astype(np.float64).T
     base = rng.standard_normal((M, N)).astype(np.float32)
-    At = torch.from_numpy(A).to(dev(), tdt)
-    Wt = torch.from_numpy(W).to(dev(), tdt)
+    At = torch.from_numpy(A_dev).to(dev(), tdt)
+    Wt = torch.from_numpy(W_dev).to(dev(), tdt)
     if epi == 2:
-        out = torch.zeros(M, N, device=dev(), dtype=tdt)
+        out = torch.zeros((M + 15) // 16 * 16 if dtype == "bf16" else M, N, device=dev(), dtype=tdt)
         ref = np.maximum(ref, 0) ** 2
     elif epi == 1:
         out = torch.from_numpy(base).to(dev())
@@ -75,8 +89,23 @@ def test_gemm_parity(dtype, M, epi, NK):
     check(lib().fc_gemm(At.data_ptr(), Wt.data_ptr(), out.data_ptr(), M, N, K, code, epi, stream()), "gemm")
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
+    if epi == 2 and dtype == "bf16":
+        got = frag_unpack(got, M)
     tol = 1e-4 if dtype == "fp32" else (1e-2 if epi == 2 else 2e-4)
     np.testing.assert_allclose(got, ref, rtol=tol, atol=tol * max(1.0, np.abs(ref).max()))
+
+
+def test_pack_operand_matches_host_layout():
+    """fc_pack_operand reproduces the documented fragment order (host
+    restatement frag_pack), including the zero padding rows."""
+    from flaxchat_amd.runtime import frag_pack
+    rng = np.random.default_rng(7)
+    a = bf(rng.standard_normal((40, 96)).astype(np.float32))
+    src = torch.from_numpy(a).to(dev(), torch.bfloat16)
+    dst = torch.full((48, 96), 3.0, device=dev(), dtype=torch.bfloat16)
+    check(lib().fc_pack_operand(src.data_ptr(), dst.data_ptr(), 40, 96, stream()), "pack")
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.float().cpu().numpy(), frag_pack(a))
 
 
 # ---------------------------------------------------------------- attention
@@ -131,25 +160,35 @@ def test_attention_parity(dtype, B, W, H, G, window, lmax):
     else:
         tdt, code = torch.float32, _lib.FC_F32
     ref = _attn_ref(q.astype(np.float64), K.astype(np.float64), V.astype(np.float64), start, nvalid, W, H, G, window)
-    qt = torch.from_numpy(q).to(dev(), tdt)
+    # packed layout: row b's nvalid[b] queries (its last slots) at row_off[b]..
+    off = np.zeros(B + 1, np.int32)
+    off[1:] = np.cumsum(nvalid)
+    tot = int(off[-1])
+    qp = np.concatenate([q[b, W - nvalid[b]:] for b in range(B)])
+    refp = np.concatenate([ref[b, W - nvalid[b]:] for b in range(B)])
+    qt = torch.from_numpy(qp).to(dev(), tdt)
     Kt = torch.from_numpy(K).to(dev(), tdt)
     Vt = torch.from_numpy(_to_vblocked(V)).to(dev(), tdt)
-    y = torch.full((B, W, H, d), 7.0, device=dev(), dtype=tdt)
+    # bf16 output is the c_proj GEMM operand: fragment order, whole 16-row blocks
+    rows = (tot + 3 + 15) // 16 * 16 if dtype == "bf16" else tot + 3
+    y = torch.full((rows, H * d), 7.0, device=dev(), dtype=tdt)
     st = torch.from_numpy(start).to(dev())
-    nv = torch.from_numpy(nvalid).to(dev())
+    ro = torch.from_numpy(off).to(dev())
     max_keys = min(cap, window + W) if window > 0 else cap
     nb = lib().fc_attention_workspace_bytes(B, W, H, G, d, max_keys)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev())
     check(lib().fc_attention(qt.data_ptr(), Kt.data_ptr(), Vt.data_ptr(), y.data_ptr(), B, W, H, G, d, cap,
-                             st.data_ptr(), nv.data_ptr(), window, max_keys, code, ws.data_ptr(), ws.numel(),
+                             ro.data_ptr(), st.data_ptr(), window, max_keys, code, ws.data_ptr(), ws.numel(),
                              stream()), "attention")
     torch.cuda.synchronize()
     got = y.float().cpu().numpy()
-    for b in range(B):
-        got_inv = got[b, :W - nvalid[b]]
-        assert np.all(got_inv == 0), "invalid slots must be zero"
+    if dtype == "bf16":
+        from flaxchat_amd.runtime import frag_unpack
+        got = frag_unpack(got, rows)
+    got = got.reshape(rows, H, d)
+    assert np.all(got[tot:] == 7.0), "rows past the chunk total must be untouched"
     tol = 1e-5 if dtype == "fp32" else 2e-2
-    np.testing.assert_allclose(got, ref, rtol=tol, atol=tol)
+    np.testing.assert_allclose(got[:tot], refp, rtol=tol, atol=tol)
 
 
 # ---------------------------------------------------------------- row stats / top-k

@@ -346,3 +346,23 @@ def test_gumbel_uniform_strictly_inside_unit_interval():
     assert np.all(u > 0) and np.all(u < 1)
     g = S.gumbel(1 << 16, 2, 0, 0, 0)
     assert np.all(np.isfinite(g))
+
+
+def test_fragment_order_layout():
+    """The fragment-order index math (include/flaxchat_amd.h) against the
+    definition written element by element: byte 16*l of block (rb, ks) is row
+    rb*16 + l%16, k = ks*32 + 8*(l//16) .. +7; frag_unpack inverts frag_pack."""
+    from flaxchat_amd.runtime import frag_pack, frag_unpack
+    R, K = 37, 96
+    a = np.arange(R * K, dtype=np.float32).reshape(R, K)
+    p = frag_pack(a).reshape(-1)
+    R16 = 48
+    assert p.size == R16 * K
+    for rb in range(R16 // 16):
+        for ks in range(K // 32):
+            for lane in range(64):
+                for e in range(8):
+                    r, k = rb * 16 + lane % 16, ks * 32 + 8 * (lane // 16) + e
+                    want = a[r, k] if r < R else 0.0
+                    assert p[((rb * (K // 32) + ks) * 64 + lane) * 8 + e] == want
+    assert np.array_equal(frag_unpack(frag_pack(a), R), a)
