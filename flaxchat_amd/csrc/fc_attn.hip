@@ -27,6 +27,19 @@
 #include "fc_common.h"
 #include "fc_internal.h"
 
+// K cache of the matrix-core path (bf16, head_dim 128): 32-key blocks of
+// 8 KB in the fragment order of the S^T = K Q^T product. In a block, load
+// (cc, s) of lane l = r + 16 g (1 KB contiguous) holds key
+// 8 (r / 4) + r % 4 + 4 cc, dims 32 s + 8 g .. +7; so element (key kk of
+// the block, dim d) sits at ((2 s + cc) 64 + r + 16 g) 8 + d % 8 with
+// s = d / 32, g = (d / 8) % 4, r = 4 (kk / 8) + kk % 4, cc = (kk / 4) % 2.
+__device__ __forceinline__ int64_t kblk_idx(int pos, int d) {
+  const int kk = pos & 31;
+  const int r = ((kk >> 3) << 2) | (kk & 3), cc = (kk >> 2) & 1;
+  const int s = d >> 5, g = (d >> 3) & 3;
+  return (int64_t)(pos >> 5) * 4096 + ((((s << 1) | cc) << 6) + r + (g << 4)) * 8 + (d & 7);
+}
+
 // ---------------------------------------------------------------------------
 // Prologue: one wave per (packed token m, head slot hh in [0, H + 2G)).
 // ---------------------------------------------------------------------------
@@ -38,7 +51,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
                                                   int D, T* __restrict__ kc, T* __restrict__ vc, int Mcap,
                                                   const int* __restrict__ Mdev, int H, int G, int hd, int cap,
                                                   const int* __restrict__ tok_row, const int* __restrict__ tok_pos,
-                                                  T* __restrict__ q) {
+                                                  T* __restrict__ q, int kblk) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int NH = H + 2 * G;
   const int64_t item = (int64_t)blockIdx.x * 4 + wave;
@@ -68,9 +81,14 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
       }
     } else if (act && pos < cap) {
       const int g = hh - H;
-      T* ko = kc + (((int64_t)b * G + g) * cap + pos) * hd;
-      st<T>(ko, lane, y1);
-      st<T>(ko, lane + half, y2);
+      T* kg = kc + ((int64_t)b * G + g) * cap * hd;
+      if (kblk) {
+        st<T>(kg, kblk_idx(pos, lane), y1);
+        st<T>(kg, kblk_idx(pos, lane + half), y2);
+      } else {
+        st<T>(kg, (int64_t)pos * hd + lane, y1);
+        st<T>(kg, (int64_t)pos * hd + lane + half, y2);
+      }
     }
   } else {
     const int g = hh - H - G;
@@ -107,13 +125,13 @@ int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const
     bf16_t* vc = (bf16_t*)c->v + layer_elems * layer;
     hipLaunchKernelGGL(k_prologue<bf16_t>, grid, dim3(256), 0, s, qkv, (const bf16_t*)h, tokens, m->rope_cos,
                        m->rope_sin, m->rope_len, (const bf16_t*)L.ve, L.ve_gate, m->n_embd, kc, vc, Mcap, Mdev, H, G,
-                       hd, c->cap, tok_row, tok_pos, (bf16_t*)q);
+                       hd, c->cap, tok_row, tok_pos, (bf16_t*)q, hd == 128 ? 1 : 0);
   } else {
     float* kc = (float*)c->k + layer_elems * layer;
     float* vc = (float*)c->v + layer_elems * layer;
     hipLaunchKernelGGL(k_prologue<float>, grid, dim3(256), 0, s, qkv, (const float*)h, tokens, m->rope_cos,
                        m->rope_sin, m->rope_len, (const float*)L.ve, L.ve_gate, m->n_embd, kc, vc, Mcap, Mdev, H, G,
-                       hd, c->cap, tok_row, tok_pos, (float*)q);
+                       hd, c->cap, tok_row, tok_pos, (float*)q, 0);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
@@ -130,14 +148,69 @@ __device__ __forceinline__ uint32_t pack2bf(float lo, float hi) {
   return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
 }
 
-__global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
-                                                   const bf16_t* __restrict__ vc, float* __restrict__ part_o,
-                                                   float* __restrict__ part_ml, int H, int G, int cap,
-                                                   const int* __restrict__ row_off, const int* __restrict__ start,
-                                                   int window, int split_keys, int nsplit, int nqblk,
-                                                   float scale_log2) {
+// One 32-key tile of one wave: scores S^T = K Q^T, online softmax update,
+// O^T += V^T P^T (see the kernel comment).
+__device__ __forceinline__ void attn_tile(const uint4 (&kf)[2][4], const uint4 (&vf)[8], const uint4 (&qf)[4],
+                                          int kb, int g4, bool cvalid, int kbeg, int kend, int lo_c, int pos_c,
+                                          float scale_log2, float& m_run, float& l_run, f32x4 (&O)[8]) {
+  f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) sc[cc] = mfma16a(kf[cc][s], qf[s], sc[cc]);
+  float p[8];
+  float mt = -INFINITY;
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int jj = i + 4 * cc;
+      const int key = kb + 8 * g4 + jj;
+      const bool ok = cvalid && key >= kbeg && key < kend && key >= lo_c && key <= pos_c;
+      p[jj] = ok ? sc[cc][i] * scale_log2 : -INFINITY;
+      mt = fmaxf(mt, p[jj]);
+    }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+  const float m_new = fmaxf(m_run, mt);
+  float alpha = 1.f, psum = 0.f;
+  if (m_new == -INFINITY) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) p[jj] = 0.f;
+  } else {
+    alpha = exp2f(m_run - m_new);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      p[jj] = exp2f(p[jj] - m_new);
+      psum += p[jj];
+    }
+  }
+  l_run = l_run * alpha + psum;
+  m_run = m_new;
+  uint4 pf;
+  pf.x = pack2bf(p[0], p[1]);
+  pf.y = pack2bf(p[2], p[3]);
+  pf.z = pack2bf(p[4], p[5]);
+  pf.w = pack2bf(p[6], p[7]);
+#pragma unroll
+  for (int db = 0; db < 8; ++db) {
+    O[db] *= alpha;
+    O[db] = mfma16a(vf[db], pf, O[db]);
+  }
+}
+
+// grid (key split, row x KV group, query block): the query block is the
+// slowest dimension, so blocks with no query (a row's second block is
+// usually empty) are dispatched last and exit at once.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+                                                       const bf16_t* __restrict__ vc, float* __restrict__ part_o,
+                                                       float* __restrict__ part_ml, bf16_t* __restrict__ y, int H,
+                                                       int G, int cap, const int* __restrict__ row_off,
+                                                       const int* __restrict__ start, int window, int split_keys,
+                                                       int nsplit, int nqblk, float scale_log2) {
   constexpr int HD = 128;
-  const int split = blockIdx.x, qb = blockIdx.y, bg = blockIdx.z;
+  const int split = blockIdx.x, bg = blockIdx.y, qb = blockIdx.z;
   const int b = bg / G, g = bg - b * G, rep = H / G;
   const int base = row_off[b], n = row_off[b + 1] - base, s0 = start[b];
   const int ncol = n * rep;
@@ -156,7 +229,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q,
     kbeg = klo + split * split_keys;
     kend = min(khi, kbeg + split_keys);
   }
-  if (kbeg >= kend) {
+  if (kbeg >= kend) {  // only with several splits: a query always sees itself
     if (threadIdx.x < 16) {
       part_ml[(pidx * 16 + threadIdx.x) * 2 + 0] = -INFINITY;
       part_ml[(pidx * 16 + threadIdx.x) * 2 + 1] = 0.f;
@@ -180,79 +253,37 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q,
   const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
   const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
   const int r = c;
-  const int krow0 = 8 * (r >> 2) + (r & 3);
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 O[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // K blocks of 32 keys in fragment order: load (cc, s) of a tile is 1 KB
+  // contiguous; V blocks are [128 dims][32 keys], one 1 KB load per db
   const int t0 = kbeg & ~31;
   const int ntiles = (kend - t0 + 31) >> 5;
-  for (int t = wave; t < ntiles; t += 4) {
+  for (int t = wave; t < ntiles; t += NW) {
     const int kb = t0 + 32 * t;
-    uint4 kf[2][4];
+    uint4 kf[2][4], vf[8];
+    const bf16_t* kt = kbase + (int64_t)(kb >> 5) * 32 * HD + lane * 8;
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-      const bf16_t* kr = kbase + (int64_t)(kb + krow0 + 4 * cc) * HD + 8 * g4;
+    for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kf[cc][s] = *(const uint4*)(kr + 32 * s);
-    }
-    uint4 vf[8];
+      for (int s = 0; s < 4; ++s) kf[cc][s] = *(const uint4*)(kt + (s * 2 + cc) * 512);
     const bf16_t* vt = vbase + (int64_t)(kb >> 5) * HD * 32 + r * 32 + 8 * g4;
 #pragma unroll
     for (int db = 0; db < 8; ++db) vf[db] = *(const uint4*)(vt + db * 16 * 32);
-
-    f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sc[cc] = mfma16a(kf[cc][s], qf[s], sc[cc]);
-    float p[8];
-    float mt = -INFINITY;
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int jj = i + 4 * cc;
-        const int key = kb + 8 * g4 + jj;
-        const bool ok = cvalid && key >= kbeg && key < kend && key >= lo_c && key <= pos_c;
-        p[jj] = ok ? sc[cc][i] * scale_log2 : -INFINITY;
-        mt = fmaxf(mt, p[jj]);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
-    const float m_new = fmaxf(m_run, mt);
-    float alpha = 1.f, psum = 0.f;
-    if (m_new == -INFINITY) {
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) p[jj] = 0.f;
-    } else {
-      alpha = exp2f(m_run - m_new);
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        p[jj] = exp2f(p[jj] - m_new);
-        psum += p[jj];
-      }
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    uint4 pf;
-    pf.x = pack2bf(p[0], p[1]);
-    pf.y = pack2bf(p[2], p[3]);
-    pf.z = pack2bf(p[4], p[5]);
-    pf.w = pack2bf(p[6], p[7]);
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      O[db] *= alpha;
-      O[db] = mfma16a(vf[db], pf, O[db]);
-    }
+    attn_tile(kf, vf, qf, kb, g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
   }
-  // merge the four waves
+  // merge the NW waves in LDS; thread t < 256 then owns column t / 16 and
+  // dims 8 (t % 16) .. +7. A single key split writes y directly (normalised,
+  // in the c_proj operand layout); otherwise the unnormalised partial and its
+  // (max, sum) go to k_attn_combine.
   float l_tot = l_run + __shfl_xor(l_run, 16, WAVE);
   l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
-  __shared__ float sm[4][16], sl[4][16];
-  __shared__ float so[4][16][HD + 4];
+  __shared__ float sm[NW][16], sl[NW][16];
+  __shared__ float so[NW][16][HD + 4];
   if (g4 == 0) {
     sm[wave][c] = m_run;
     sl[wave][c] = l_tot;
@@ -262,25 +293,41 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const bf16_t* __restrict__ q,
 #pragma unroll
     for (int i = 0; i < 4; ++i) so[wave][c][16 * db + 4 * g4 + i] = O[db][i];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * HD; idx += 256) {
-    const int qc = idx / HD, d = idx - qc * HD;
-    float M = -INFINITY;
+  if (threadIdx.x >= 256) return;
+  const int qc = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+  float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][qc]);
-    float o = 0.f, L = 0.f;
-    if (M != -INFINITY) {
+  for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w][qc]);
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+  if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float a = exp2f(sm[w][qc] - M);
-        o += a * so[w][qc][d];
-        L += a * sl[w][qc];
-      }
+    for (int w = 0; w < NW; ++w) {
+      const float a = exp2f(sm[w][qc] - M);
+      L += a * sl[w][qc];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] += a * so[w][qc][d0 + i];
     }
-    part_o[(pidx * 16 + qc) * HD + d] = o;
-    if (d == 0) {
-      part_ml[(pidx * 16 + qc) * 2 + 0] = M;
-      part_ml[(pidx * 16 + qc) * 2 + 1] = L;
-    }
+  }
+  if (nsplit == 1) {
+    const int colq = qb * 16 + qc;
+    if (colq >= ncol) return;
+    const int jq = colq / rep, hq = g * rep + (colq - jq * rep);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint4 pk;
+    pk.x = pack2bf(o[0] * inv, o[1] * inv);
+    pk.y = pack2bf(o[2] * inv, o[3] * inv);
+    pk.z = pack2bf(o[4] * inv, o[5] * inv);
+    pk.w = pack2bf(o[6] * inv, o[7] * inv);
+    *(uint4*)(y + frag_idx(base + jq, hq * HD + d0, H * HD)) = pk;
+    return;
+  }
+  float4* po = (float4*)(part_o + (pidx * 16 + qc) * HD + d0);
+  po[0] = make_float4(o[0], o[1], o[2], o[3]);
+  po[1] = make_float4(o[4], o[5], o[6], o[7]);
+  if (d0 == 0) {
+    part_ml[(pidx * 16 + qc) * 2 + 0] = M;
+    part_ml[(pidx * 16 + qc) * 2 + 1] = L;
   }
 }
 
@@ -292,7 +339,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
                                                       const float* __restrict__ part_ml, T* __restrict__ y, int H,
                                                       int G, int nqblk, int nsplit, const int* __restrict__ row_off) {
   constexpr int HD = 128;
-  const int qb = blockIdx.x, bg = blockIdx.y;
+  const int bg = blockIdx.x, qb = blockIdx.y;
   const int b = bg / G, g = bg - b * G, rep = H / G;
   const int base = row_off[b], ncol = (row_off[b + 1] - base) * rep;
   const int c = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
@@ -389,6 +436,16 @@ __global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, cons
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// Workgroups a typical attention launch is split into (key splits x rows x
+// KV groups x query blocks).
+#ifndef FC_ATTN_TARGET_WG
+#define FC_ATTN_TARGET_WG 256
+#endif
+// waves per attention workgroup (they take the block's 32-key tiles round robin)
+#ifndef FC_ATTN_WAVES
+#define FC_ATTN_WAVES 4
+#endif
+
 AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, int n_kv_head, int max_keys) {
   AttnGrid a;
   const int rep = n_head / n_kv_head;
@@ -398,7 +455,7 @@ AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, i
   const int typ_blk = std::min(a.nqblk, std::max(1, (typ_per_row * rep + 15) / 16));
   const int64_t units = (int64_t)batch * n_kv_head * typ_blk;
   const int range = max(max_keys, 1);
-  int want = (int)((1024 + units - 1) / units);
+  int want = (int)((FC_ATTN_TARGET_WG + units - 1) / units);
   want = max(1, min(want, (range + 127) / 128));
   int sk = (range + want - 1) / want;
   sk = max(128, (sk + 127) / 128 * 128);
@@ -409,11 +466,11 @@ AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, i
 
 int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head, int head_dim, int max_keys) {
   if (head_dim != 128) return 0;
-  // fc_attn_grid never makes more splits than ceil(1024 / units), and one
-  // token per row gives the fewest units
+  // fc_attn_grid never makes more splits than ceil(FC_ATTN_TARGET_WG /
+  // units), and one token per row gives the fewest units
   AttnGrid a = fc_attn_grid(batch, max_per_row, 1, n_head, n_kv_head, max_keys);
   const int64_t units1 = (int64_t)batch * n_kv_head;
-  const int64_t nsplit = std::max<int64_t>(a.nsplit, (1024 + units1 - 1) / units1);
+  const int64_t nsplit = std::max<int64_t>(a.nsplit, (FC_ATTN_TARGET_WG + units1 - 1) / units1);
   const int64_t units = (int64_t)batch * n_kv_head * a.nqblk * nsplit * 16;
   return fc_align(units * 128 * 4) + fc_align(units * 2 * 4);
 }
@@ -432,12 +489,15 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
                  "attention workspace too small");
     float* po = (float*)part;
     float* pml = (float*)((char*)part + fc_align(units * 128 * 4));
-    hipLaunchKernelGGL(k_attn_mfma, dim3(a.nsplit, a.nqblk, B * G), dim3(256), 0, s, (const bf16_t*)q,
-                       (const bf16_t*)kc, (const bf16_t*)vc, po, pml, H, G, cap, row_off, start, window, a.split_keys,
-                       a.nsplit, a.nqblk, scale * 1.4426950408889634f);
-    FC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3(a.nqblk, B * G), dim3(256), 0, s, po, pml, (bf16_t*)y, H, G,
-                       a.nqblk, a.nsplit, row_off);
+    FC_CHECK_ARG(B * G <= 65535, "batch * n_kv_head must be <= 65535");
+    hipLaunchKernelGGL(k_attn_mfma<FC_ATTN_WAVES>, dim3(a.nsplit, B * G, a.nqblk), dim3(64 * FC_ATTN_WAVES), 0, s,
+                       (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, po, pml, (bf16_t*)y, H, G, cap, row_off,
+                       start, window, a.split_keys, a.nsplit, a.nqblk, scale * 1.4426950408889634f);
+    if (a.nsplit > 1) {
+      FC_LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3(B * G, a.nqblk), dim3(256), 0, s, po, pml, (bf16_t*)y, H, G,
+                         a.nqblk, a.nsplit, row_off);
+    }
   } else {
     FC_CHECK_ARG(hd <= 128, "head_dim must be <= 128");
     FC_CHECK_ARG(max_keys <= VALU_MAXK, "VALU attention supports at most 8192 visible keys");

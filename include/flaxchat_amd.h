@@ -21,7 +21,12 @@
  *                    1 KB in [row block][k step] order; byte 16*l of a block
  *                    holds row l % 16, k = 8*(l/16) .. +7 of the step.
  *                    fc_pack_operand converts a row-major matrix.
- *   K cache          [layer][batch][kv_head][cap][head_dim]
+ *   K cache          [layer][batch][kv_head][cap][head_dim]; with bf16 and
+ *                    head_dim 128 (the matrix-core attention) each 32-position
+ *                    block of 8 KB is in the fragment order of the K.Q^T
+ *                    product: position 32 B + kk, dim d at element
+ *                    B*4096 + ((2*(d/32) + (kk/4)%2)*64 + 4*(kk/8) + kk%4
+ *                    + 16*((d/8)%4))*8 + d%8
  *   V cache          [layer][batch][kv_head][cap/32][head_dim][32]
  *                    (32-position blocks stored transposed so that the
  *                    P·V matrix-core operand is one 16-byte load per lane)

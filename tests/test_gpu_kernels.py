@@ -133,6 +133,21 @@ def _to_vblocked(V):
     return np.ascontiguousarray(V.reshape(B, G, cap // 32, 32, d).transpose(0, 1, 2, 4, 3))
 
 
+def _to_kblocked(K):
+    """K cache of the matrix-core attention (include/flaxchat_amd.h): in each
+    32-position block, element (kk, d) at ((2*(d//32) + (kk//4)%2)*64 +
+    4*(kk//8) + kk%4 + 16*((d//8)%4))*8 + d%8."""
+    B, G, cap, d = K.shape
+    assert d == 128
+    out = np.zeros((B, G, cap // 32, 4096), K.dtype)
+    kk = np.arange(32)[:, None]
+    dd = np.arange(128)[None, :]
+    idx = ((2 * (dd // 32) + (kk // 4) % 2) * 64 + 4 * (kk // 8) + kk % 4 + 16 * ((dd // 8) % 4)) * 8 + dd % 8
+    blocks = K.reshape(B, G, cap // 32, 32, 128)
+    out[..., idx.reshape(-1)] = blocks.reshape(B, G, cap // 32, 32 * 128)
+    return out.reshape(B, G, cap, d)
+
+
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 @pytest.mark.parametrize("B,W,H,G,window,lmax", [
     (4, 5, 6, 6, 0, 700),       # verify chunk, full layer
@@ -141,6 +156,8 @@ def _to_vblocked(V):
     (5, 1, 6, 6, 0, 1500),      # draft step
     (2, 40, 2, 2, 64, 300),     # prefill-like chunk, many query blocks
     (3, 3, 4, 2, 0, 70),        # ragged, short rows
+    (32, 2, 8, 8, 0, 300),      # >= 256 row x group units: one key split, output written directly
+    (32, 3, 16, 8, 100, 300),   # the same with GQA 2:1 and a window
 ])
 def test_attention_parity(dtype, B, W, H, G, window, lmax):
     _say(f"attention dtype={dtype} B={B} W={W} H={H} G={G} window={window} lmax={lmax}")
@@ -167,7 +184,7 @@ def test_attention_parity(dtype, B, W, H, G, window, lmax):
     qp = np.concatenate([q[b, W - nvalid[b]:] for b in range(B)])
     refp = np.concatenate([ref[b, W - nvalid[b]:] for b in range(B)])
     qt = torch.from_numpy(qp).to(dev(), tdt)
-    Kt = torch.from_numpy(K).to(dev(), tdt)
+    Kt = torch.from_numpy(_to_kblocked(K) if dtype == "bf16" else K).to(dev(), tdt)
     Vt = torch.from_numpy(_to_vblocked(V)).to(dev(), tdt)
     # bf16 output is the c_proj GEMM operand: fragment order, whole 16-row blocks
     rows = (tot + 3 + 15) // 16 * 16 if dtype == "bf16" else tot + 3
