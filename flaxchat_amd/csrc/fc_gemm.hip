@@ -156,22 +156,35 @@ __device__ __forceinline__ f32x4 mfma16(v4u a, v4u b, f32x4 c) {
 // tiles are summed in LDS at the end and the epilogue runs on a coalesced
 // row-major layout.
 //
-// Grid: 1-D over (N tile, K split, M tile). Workgroups are dealt to the
-// eight XCDs round robin, so N tile n lands on XCD n % 8 and, within an XCD,
-// the M tiles of one N tile are consecutive: the weight slab they share is
-// read from HBM once and hit in that XCD's L2 by the others. The row count
-// may live on the device (`Mdev`, at most Mcap): tiles past it exit at once.
+// Grid: 1-D over (N tile, K split, M tile), the N tile count padded to a
+// multiple of 8. Workgroups are dealt to the eight XCDs round robin and both
+// tile orders keep N tile n on XCD n % 8, so the M tiles that share its
+// weight slab read it from HBM once and hit in that XCD's L2:
+//   mfast = 1: within an XCD the M tiles of one N tile run back to back
+//              (wide N, e.g. lm_head: the slab is reused while still in L2);
+//   mfast = 0: M tile slowest; with a device row count (`Mdev`, at most
+//              Mcap) the tiles past it come last in dispatch order and exit
+//              at once.
 template <int MB, int NB, int NS, int EPI, bool PK = false>
 __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
                                                  int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
-                                                 int S, int mtiles, Epi e) {
+                                                 int S, int mtiles, int mfast, Epi e) {
   constexpr int MT = 16 * MB, NT = 16 * NB;
   const int id = blockIdx.x;
-  const int xcd = id & 7, loc = id >> 3;
-  const int per = S * mtiles;
-  const int nl = loc / per, rem = loc - nl * per;
-  const int s = rem / mtiles, mt = rem - s * mtiles;
-  const int nt = nl * 8 + xcd;
+  const int ntiles8 = (ntiles + 7) & ~7;
+  int nt, s, mt;
+  if (mfast) {  // per XCD: the M tiles of one N tile back to back
+    const int xcd = id & 7, loc = id >> 3, per = S * mtiles;
+    const int nl = loc / per, rem = loc - nl * per;
+    s = rem / mtiles;
+    mt = rem - s * mtiles;
+    nt = nl * 8 + xcd;
+  } else {      // M tile slowest
+    nt = id % ntiles8;
+    const int rest = id / ntiles8;
+    s = rest % S;
+    mt = rest / S;
+  }
   if (nt >= ntiles) return;
   const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
   const int m0 = mt * MT;
@@ -315,9 +328,10 @@ static void launch_ks(const void* A, const void* W, int Mcap, const int* Mdev, i
                       hipStream_t s) {
   const int ntiles = N / (16 * NB), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
   const int nwg = (ntiles + 7) / 8 * 8 * S * mtiles;
+  const int mfast = Mdev == nullptr ? 1 : 0;
   FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_ks<MB, NB, FC_GEMM_NS, E, PK>), dim3(nwg), dim3(256), 0, s,
                                            (const bf16_t*)A, (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, S, mtiles,
-                                           e));
+                                           mfast, e));
 }
 
 // One plan drives the workspace sizing and the launch. The tile shape and
@@ -327,6 +341,8 @@ struct GemmPlan {
   bool gemv;
   int mb, nb, S;
 };
+// Tile shape and K split by typical row count, from sweeps on MI355X at the
+// engine's shapes (N = 1536 / 4608 / 6144 / 65536, K = 1536 / 6144).
 static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
   GemmPlan p{};
   p.S = 1;
@@ -334,25 +350,28 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     p.gemv = true;
     return p;
   }
-  p.mb = Mtyp <= 16 ? 1 : (Mtyp <= 32 ? 2 : 4);
-  const int mtiles = (Mtyp + 16 * p.mb - 1) / (16 * p.mb);
-  // widest column tile that still gives >= 256 workgroups, else the
-  // narrowest allowed one plus a K split when the output allows it
-  const int nb_min = p.mb == 2 ? 1 : 2;
-  p.nb = nb_min;
-  for (int nb = 4; nb >= nb_min; nb /= 2)
-    if (N % (16 * nb) == 0 && (N / (16 * nb)) * mtiles >= 256) {
-      p.nb = nb;
-      break;
-    }
-  if (N % (16 * p.nb) != 0) p.nb = 2;
-  const int wgs = (N / (16 * p.nb)) * mtiles;
-  if (can_split && wgs < 256) {
-    const int C = K / 64;
-    int S = (256 + wgs - 1) / wgs;
-    S = std::min(S, std::max(1, C / 4));  // keep >= 1 chunk per wave
-    p.S = std::max(1, std::min(S, FC_MAX_SPLIT));
+  const int C = K / 64;
+  const int s_max = std::max(1, std::min(C / 4, FC_MAX_SPLIT));  // >= 1 chunk per wave
+  if (Mtyp <= 16) {
+    // one 16-row tile: fill the GPU with column tiles and K splits
+    p.mb = 1;
+    p.nb = 4;
+    const int wgs = N / 64;
+    if (can_split && wgs < 256) p.S = std::min((256 + wgs - 1) / wgs, s_max);
+  } else if (Mtyp <= 32) {
+    p.mb = 2;
+    p.nb = 2;
+    if (can_split) p.S = std::min(K > 2048 ? 4 : 2, s_max);
+  } else if (can_split && K > 2048) {
+    p.mb = 4;
+    p.nb = 4;
+    p.S = std::min(2, s_max);
+  } else {
+    p.mb = 2;
+    p.nb = 4;
   }
+  while (p.nb > 1 && N % (16 * p.nb) != 0) p.nb /= 2;
+  if (p.nb == 1 && p.mb != 2) p.nb = 2;  // instantiated shapes: (1,2|4), (2,1|2|4), (4,2|4)
   return p;
 }
 
