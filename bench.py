@@ -16,11 +16,13 @@ every row has its max_tokens) are timed between two synchronisations.
 value = tokens emitted in the timed rounds (accepted drafts + corrections +
 bonus tokens, counted up to max_tokens per row) / timed seconds.
 
-roofline: the verify-pass attention (split-KV flash-decode, the dominant
-HBM consumer) timed with HIP events on the engine's stream, at the state the
-timed run ends in, over one S (window 1024) and one L (full) layer weighted
-18:6 like the d24 SSSL stack. Algorithmic bytes per launch = the distinct
-visible K and V bytes of every row (read once) + Q + O.
+roofline: the verify-pass attention (flash-decode, the dominant HBM
+consumer) timed with HIP events on the engine's stream, at the state the
+timed run ends in, walking every layer's cache in turn (so the 256 MB
+Infinity Cache holds no layer between calls, as in a real round); S
+(window 1024) and L (full) layers are timed apart and weighted 18:6 like the
+d24 SSSL stack. Algorithmic bytes per launch = the distinct visible K and V
+bytes of every row (read once) + Q + O.
 
 cpu_baseline: the CPU restatement of the reference algorithm (oracle/,
 literal mode: token-by-token verify and full re-prefill on rejection) on
@@ -56,9 +58,11 @@ HBM_PEAK_GBS = 8000.0
 ATTN_TRAFFIC_RATIO = 1.14
 
 
-def attention_roofline(sess, n_iter=20):
+def attention_roofline(sess, n_rep=3):
     """Time the verify attention at the session's current lengths: every row
-    feeds k+1 queries (one pending token and k drafts) at its cache length."""
+    feeds k+1 queries (one pending token and k drafts) at its cache length.
+    Each timed pass walks all layers in order (7.4 GB of K/V at cfg4), so no
+    layer is served from the 256 MB Infinity Cache, as in a real round."""
     import torch
     from flaxchat_amd import _lib
     T = sess.T
@@ -68,44 +72,53 @@ def attention_roofline(sess, n_iter=20):
     s = sess.stream
     t_len = sess.bufs["t_len"].cpu().numpy().astype(np.int64)
     q = torch.randn(B * W, T.H, T.hd, device=dev).to(torch.bfloat16)
-    y = torch.empty_like(q)
+    y = torch.empty(((B * W + 15) // 16 * 16, T.H * T.hd), device=dev, dtype=torch.bfloat16)
     start = sess.bufs["t_len"].clone()
     row_off = torch.arange(0, B * W + 1, W, dtype=torch.int32, device=dev)
     cap = sess.tcache.cap
-    res = {}
     es = 2
     layer_elems = B * T.G * cap * T.hd
-    for name, layer in (("S", 0), ("L", T.L - 1)):
+    launches = []
+    for layer in range(T.L):
         win = T.windows[layer]
         max_keys = min(cap, win + W) if win > 0 else cap
         nb = _lib.lib().fc_attention_workspace_bytes(B, W, T.H, T.G, T.hd, max_keys)
-        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
-        kp = sess.tcache.k.data_ptr() + layer * layer_elems * es
-        vp = sess.tcache.v.data_ptr() + layer * layer_elems * es
-        def launch():
-            _lib.check(_lib.lib().fc_attention(q.data_ptr(), kp, vp, y.data_ptr(), B, W, T.H, T.G, T.hd, cap,
+        launches.append((layer, win, max_keys, torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)))
+
+    def run_all(sel):
+        for layer, win, max_keys, ws in launches:
+            if not sel(win):
+                continue
+            kp = sess.tcache.k.data_ptr() + layer * layer_elems * es
+            vp = sess.tcache.v.data_ptr() + layer * layer_elems * es
+            _lib.check(_lib.lib().fc_attention(q.data_ptr(), kp, vp, y.data_ptr(), B, B * W, W, T.H, T.G, T.hd, cap,
                                                row_off.data_ptr(), start.data_ptr(), win, max_keys, 1,
                                                ws.data_ptr(), ws.numel(), s.cuda_stream), "attention")
+
+    torch.cuda.synchronize()  # inputs above were made on the default stream; the launches use the engine's
+    res = {}
+    short = lambda w: 0 < w < T.config.sequence_len
+    for name, sel in (("S", short), ("L", lambda w: not short(w))):
+        n_layers = sum(1 for _, w, _, _ in launches if sel(w))
         with torch.cuda.stream(s):
-            for _ in range(3):
-                launch()
+            run_all(sel)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-            for _ in range(n_iter):
-                launch()
+            for _ in range(n_rep):
+                run_all(sel)
             e1.record(s)
         e1.synchronize()
-        ms = e0.elapsed_time(e1) / n_iter
+        ms = e0.elapsed_time(e1) / (n_rep * n_layers)
+        win = next(w for _, w, _, _ in launches if sel(w))
         # distinct visible keys per row: full layer 0..pos_last; window layer
         # from max(0, pos_first - window) to pos_last
         pos_last = t_len + W - 1
-        lo = np.maximum(0, t_len - win) if win > 0 else np.zeros_like(t_len)
+        lo = np.maximum(0, t_len - win) if short(win) else np.zeros_like(t_len)
         keys = (pos_last - lo + 1).sum()
         kv_bytes = keys * T.G * T.hd * 2 * es
         qo_bytes = 2 * B * W * T.H * T.hd * es
-        res[name] = dict(ms=ms, bytes=int(kv_bytes + qo_bytes))
-    nS = sum(1 for w in T.windows if w > 0 and w < T.config.sequence_len)
-    nL = T.L - nS
+        res[name] = dict(ms=ms, bytes=int(kv_bytes + qo_bytes), layers=n_layers)
+    nS, nL = res["S"]["layers"], res["L"]["layers"]
     tot_b = nS * res["S"]["bytes"] + nL * res["L"]["bytes"]
     tot_s = (nS * res["S"]["ms"] + nL * res["L"]["ms"]) / 1e3
     return dict(achieved=tot_b / tot_s / 1e9, per_launch_bytes=tot_b / T.L, per_launch_us=tot_s / T.L * 1e6,

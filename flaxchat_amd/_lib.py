@@ -84,7 +84,8 @@ def _declare(L):
     L.fc_pack_operand.restype = i32
     L.fc_attention_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32]
     L.fc_attention_workspace_bytes.restype = i64
-    L.fc_attention.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64, vp]
+    L.fc_attention.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64,
+                               vp]
     L.fc_spec_workspace_bytes.argtypes = [POINTER(FcModel), POINTER(FcModel), i32, i32]
     L.fc_spec_workspace_bytes.restype = i64
     L.fc_attention.restype = i32

@@ -27,6 +27,10 @@
 #include "fc_common.h"
 #include "fc_internal.h"
 
+#ifndef FC_ATTN_PIPE
+#define FC_ATTN_PIPE 0
+#endif
+
 // K cache of the matrix-core path (bf16, head_dim 128): 32-key blocks of
 // 8 KB in the fragment order of the S^T = K Q^T product. In a block, load
 // (cc, s) of lane l = r + 16 g (1 KB contiguous) holds key
@@ -48,7 +52,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
                                                   const int* __restrict__ tokens, const float* __restrict__ rcos,
                                                   const float* __restrict__ rsin, int rope_len,
                                                   const T* __restrict__ ve, const float* __restrict__ ve_gate,
-                                                  int D, T* __restrict__ kc, T* __restrict__ vc, int Mcap,
+                                                  int D, T* __restrict__ kc, T* __restrict__ vc, int B, int Mcap,
                                                   const int* __restrict__ Mdev, int H, int G, int hd, int cap,
                                                   const int* __restrict__ tok_row, const int* __restrict__ tok_pos,
                                                   T* __restrict__ q, int kblk) {
@@ -59,6 +63,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
   const int m = (int)(item / NH), hh = (int)(item % NH);
   if (m >= *Mdev) return;
   const int b = tok_row[m], pos = tok_pos[m];
+  if ((unsigned)b >= (unsigned)B) return;
   const int half = hd >> 1;
   const bool act = lane < half;
   const float* row = qkv + ((int64_t)m * NH + hh) * hd;
@@ -79,7 +84,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
         st<T>(qo, lane, y1);
         st<T>(qo, lane + half, y2);
       }
-    } else if (act && pos < cap) {
+    } else if (act && pos >= 0 && pos < cap) {
       const int g = hh - H;
       T* kg = kc + ((int64_t)b * G + g) * cap * hd;
       if (kblk) {
@@ -103,7 +108,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
         x2 = x2 + gate * ld<T>(vr, lane + half);
       }
     }
-    if (act && pos < cap) {
+    if (act && pos >= 0 && pos < cap) {
       T* vb = vc + ((((int64_t)b * G + g) * (cap / 32) + pos / 32) * hd) * 32;
       st<T>(vb, (int64_t)lane * 32 + (pos & 31), x1);
       st<T>(vb, (int64_t)(lane + half) * 32 + (pos & 31), x2);
@@ -124,13 +129,13 @@ int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const
     bf16_t* kc = (bf16_t*)c->k + layer_elems * layer;
     bf16_t* vc = (bf16_t*)c->v + layer_elems * layer;
     hipLaunchKernelGGL(k_prologue<bf16_t>, grid, dim3(256), 0, s, qkv, (const bf16_t*)h, tokens, m->rope_cos,
-                       m->rope_sin, m->rope_len, (const bf16_t*)L.ve, L.ve_gate, m->n_embd, kc, vc, Mcap, Mdev, H, G,
+                       m->rope_sin, m->rope_len, (const bf16_t*)L.ve, L.ve_gate, m->n_embd, kc, vc, c->batch, Mcap, Mdev, H, G,
                        hd, c->cap, tok_row, tok_pos, (bf16_t*)q, hd == 128 ? 1 : 0);
   } else {
     float* kc = (float*)c->k + layer_elems * layer;
     float* vc = (float*)c->v + layer_elems * layer;
     hipLaunchKernelGGL(k_prologue<float>, grid, dim3(256), 0, s, qkv, (const float*)h, tokens, m->rope_cos,
-                       m->rope_sin, m->rope_len, (const float*)L.ve, L.ve_gate, m->n_embd, kc, vc, Mcap, Mdev, H, G,
+                       m->rope_sin, m->rope_len, (const float*)L.ve, L.ve_gate, m->n_embd, kc, vc, c->batch, Mcap, Mdev, H, G,
                        hd, c->cap, tok_row, tok_pos, (float*)q, 0);
   }
   FC_LAUNCH_CHECK();
@@ -207,12 +212,14 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
                                                        const bf16_t* __restrict__ vc, float* __restrict__ part_o,
                                                        float* __restrict__ part_ml, bf16_t* __restrict__ y, int H,
                                                        int G, int cap, const int* __restrict__ row_off,
-                                                       const int* __restrict__ start, int window, int split_keys,
-                                                       int nsplit, int nqblk, float scale_log2) {
+                                                       const int* __restrict__ start, int max_per_row, int Mcap,
+                                                       int window, int split_keys, int nsplit, int nqblk,
+                                                       float scale_log2) {
   constexpr int HD = 128;
   const int split = blockIdx.x, bg = blockIdx.y, qb = blockIdx.z;
   const int b = bg / G, g = bg - b * G, rep = H / G;
-  const int base = row_off[b], n = row_off[b + 1] - base, s0 = start[b];
+  const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
+  const int base = sp.base, n = sp.n, s0 = start[b];
   const int ncol = n * rep;
   if (qb * 16 >= ncol) return;  // no query of this row in the block: combine reads nothing here
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -263,19 +270,44 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
   // contiguous; V blocks are [128 dims][32 keys], one 1 KB load per db
   const int t0 = kbeg & ~31;
   const int ntiles = (kend - t0 + 31) >> 5;
+#define ATT_LOAD(kf, vf, kb_)                                                                      \
+  {                                                                                                \
+    const bf16_t* kt = kbase + (int64_t)((kb_) >> 5) * 32 * HD + lane * 8;                         \
+    _Pragma("unroll") for (int cc = 0; cc < 2; ++cc)                                               \
+      _Pragma("unroll") for (int s = 0; s < 4; ++s) kf[cc][s] = *(const uint4*)(kt + (s * 2 + cc) * 512); \
+    const bf16_t* vt = vbase + (int64_t)((kb_) >> 5) * HD * 32 + r * 32 + 8 * g4;                  \
+    _Pragma("unroll") for (int db = 0; db < 8; ++db) vf[db] = *(const uint4*)(vt + db * 16 * 32);  \
+  }
+#if FC_ATTN_PIPE
+  // two tiles in flight per wave: the next tile's loads are issued before the
+  // current one computes (a clamped index re-reads the last tile)
+  const int nmine = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;
+  if (nmine > 0) {
+    uint4 kA[2][4], vA[8], kB[2][4], vB[8];
+    auto kb_of = [&](int i) { return t0 + 32 * (wave + NW * min(i, nmine - 1)); };
+    ATT_LOAD(kA, vA, kb_of(0));
+    int i = 0;
+    for (; i + 1 < nmine; i += 2) {
+      ATT_LOAD(kB, vB, kb_of(i + 1));
+      __builtin_amdgcn_sched_barrier(0);
+      attn_tile(kA, vA, qf, kb_of(i), g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
+      __builtin_amdgcn_sched_barrier(0);
+      ATT_LOAD(kA, vA, kb_of(i + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      attn_tile(kB, vB, qf, kb_of(i + 1), g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < nmine) attn_tile(kA, vA, qf, kb_of(i), g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
+  }
+#else
   for (int t = wave; t < ntiles; t += NW) {
     const int kb = t0 + 32 * t;
     uint4 kf[2][4], vf[8];
-    const bf16_t* kt = kbase + (int64_t)(kb >> 5) * 32 * HD + lane * 8;
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kf[cc][s] = *(const uint4*)(kt + (s * 2 + cc) * 512);
-    const bf16_t* vt = vbase + (int64_t)(kb >> 5) * HD * 32 + r * 32 + 8 * g4;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) vf[db] = *(const uint4*)(vt + db * 16 * 32);
+    ATT_LOAD(kf, vf, kb);
     attn_tile(kf, vf, qf, kb, g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
   }
+#endif
+#undef ATT_LOAD
   // merge the NW waves in LDS; thread t < 256 then owns column t / 16 and
   // dims 8 (t % 16) .. +7. A single key split writes y directly (normalised,
   // in the c_proj operand layout); otherwise the unnormalised partial and its
@@ -337,11 +369,13 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
 template <typename T>
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
                                                       const float* __restrict__ part_ml, T* __restrict__ y, int H,
-                                                      int G, int nqblk, int nsplit, const int* __restrict__ row_off) {
+                                                      int G, int nqblk, int nsplit, const int* __restrict__ row_off,
+                                                      int max_per_row, int Mcap) {
   constexpr int HD = 128;
   const int bg = blockIdx.x, qb = blockIdx.y;
   const int b = bg / G, g = bg - b * G, rep = H / G;
-  const int base = row_off[b], ncol = (row_off[b + 1] - base) * rep;
+  const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
+  const int base = sp.base, ncol = sp.n * rep;
   const int c = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
   const int col = qb * 16 + c;
   if (col >= ncol) return;
@@ -388,13 +422,15 @@ template <typename T>
 __global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, const T* __restrict__ kc,
                                                    const T* __restrict__ vc, T* __restrict__ y, int H, int G, int hd,
                                                    int cap, const int* __restrict__ row_off,
-                                                   const int* __restrict__ start, int window, float scale) {
+                                                   const int* __restrict__ start, int max_per_row, int Mcap,
+                                                   int window, float scale) {
   __shared__ float qs[128];
   __shared__ float sc[VALU_MAXK];
   __shared__ float red[16];
   const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int base = row_off[b];
-  if (j >= row_off[b + 1] - base) return;
+  const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
+  const int base = sp.base;
+  if (j >= sp.n) return;
   const int m = base + j;
   const int rep = H / G, g = h / rep;
   const int pos = min(start[b] + j, cap - 1);
@@ -475,9 +511,10 @@ int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head
   return fc_align(units * 128 * 4) + fc_align(units * 2 * 4);
 }
 
-int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_per_row,
-                        int typ_per_row, int H, int G, int hd, int cap, const int* row_off, const int* start,
-                        int window, int max_keys, int dtype, void* part, int64_t part_bytes, hipStream_t s) {
+int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_tokens,
+                        int max_per_row, int typ_per_row, int H, int G, int hd, int cap, const int* row_off,
+                        const int* start, int window, int max_keys, int dtype, void* part, int64_t part_bytes,
+                        hipStream_t s) {
   FC_CHECK_ARG(H % G == 0, "n_head must be a multiple of n_kv_head");
   FC_CHECK_ARG(cap % 32 == 0, "cache capacity must be a multiple of 32");
   FC_CHECK_ARG(max_per_row > 0, "max_per_row");
@@ -492,11 +529,12 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
     FC_CHECK_ARG(B * G <= 65535, "batch * n_kv_head must be <= 65535");
     hipLaunchKernelGGL(k_attn_mfma<FC_ATTN_WAVES>, dim3(a.nsplit, B * G, a.nqblk), dim3(64 * FC_ATTN_WAVES), 0, s,
                        (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, po, pml, (bf16_t*)y, H, G, cap, row_off,
-                       start, window, a.split_keys, a.nsplit, a.nqblk, scale * 1.4426950408889634f);
+                       start, max_per_row, max_tokens, window, a.split_keys, a.nsplit, a.nqblk,
+                       scale * 1.4426950408889634f);
     if (a.nsplit > 1) {
       FC_LAUNCH_CHECK();
       hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3(B * G, a.nqblk), dim3(256), 0, s, po, pml, (bf16_t*)y, H, G,
-                         a.nqblk, a.nsplit, row_off);
+                         a.nqblk, a.nsplit, row_off, max_per_row, max_tokens);
     }
   } else {
     FC_CHECK_ARG(hd <= 128, "head_dim must be <= 128");
@@ -504,10 +542,12 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
     const dim3 grid(max_per_row, H, B);
     if (dtype == FC_BF16)
       hipLaunchKernelGGL(k_attn_valu<bf16_t>, grid, dim3(256), 0, s, (const bf16_t*)q, (const bf16_t*)kc,
-                         (const bf16_t*)vc, (bf16_t*)y, H, G, hd, cap, row_off, start, window, scale);
+                         (const bf16_t*)vc, (bf16_t*)y, H, G, hd, cap, row_off, start, max_per_row, max_tokens,
+                         window, scale);
     else
       hipLaunchKernelGGL(k_attn_valu<float>, grid, dim3(256), 0, s, (const float*)q, (const float*)kc,
-                         (const float*)vc, (float*)y, H, G, hd, cap, row_off, start, window, scale);
+                         (const float*)vc, (float*)y, H, G, hd, cap, row_off, start, max_per_row, max_tokens, window,
+                         scale);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
@@ -519,12 +559,13 @@ extern "C" int64_t fc_attention_workspace_bytes(int32_t batch, int32_t max_per_r
 }
 
 extern "C" int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y, int32_t batch,
-                                int32_t max_per_row, int32_t n_head, int32_t n_kv_head, int32_t head_dim,
-                                int32_t cap, const int32_t* row_off, const int32_t* start, int32_t window,
-                                int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes, void* stream) {
+                                int32_t max_tokens, int32_t max_per_row, int32_t n_head, int32_t n_kv_head,
+                                int32_t head_dim, int32_t cap, const int32_t* row_off, const int32_t* start,
+                                int32_t window, int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes,
+                                void* stream) {
   FC_CHECK_ARG(q && kc && vc && y && row_off && start, "null pointer");
-  FC_CHECK_ARG(batch > 0 && max_per_row > 0 && n_head > 0 && n_kv_head > 0, "sizes");
+  FC_CHECK_ARG(batch > 0 && max_tokens > 0 && max_per_row > 0 && n_head > 0 && n_kv_head > 0, "sizes");
   FC_CHECK_ARG(max_keys > 0 && max_keys <= cap, "max_keys must be in [1, cap]");
-  return fc_launch_attention(q, kc, vc, y, batch, max_per_row, max_per_row, n_head, n_kv_head, head_dim, cap,
-                             row_off, start, window, max_keys, dtype, work, work_bytes, (hipStream_t)stream);
+  return fc_launch_attention(q, kc, vc, y, batch, max_tokens, max_per_row, max_per_row, n_head, n_kv_head, head_dim,
+                             cap, row_off, start, window, max_keys, dtype, work, work_bytes, (hipStream_t)stream);
 }

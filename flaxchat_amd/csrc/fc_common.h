@@ -37,6 +37,18 @@ template <> __device__ __forceinline__ int64_t act_idx<uint16_t>(int64_t r, int 
 template <> __device__ __forceinline__ int64_t act_idx<float>(int64_t r, int k, int K) { return r * K + k; }
 __host__ __device__ __forceinline__ int64_t round16(int64_t r) { return (r + 15) / 16 * 16; }
 
+// Packed tokens of row b (row_off as in fc_chunk): n = 0 when the descriptor
+// is out of range (more than max_per_row tokens, or past the capacity), so a
+// bad descriptor feeds nothing instead of addressing outside the buffers.
+struct RowSpan {
+  int base, n;
+};
+__device__ __forceinline__ RowSpan row_span(const int* row_off, int b, int max_per_row, int Mcap) {
+  const int base = row_off[b], n = row_off[b + 1] - base;
+  if (base < 0 || n <= 0 || n > max_per_row || base + n > Mcap) return RowSpan{0, 0};
+  return RowSpan{base, n};
+}
+
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i);
 template <> __device__ __forceinline__ float ld<float>(const float* p, int64_t i) { return p[i]; }
 template <> __device__ __forceinline__ float ld<bf16_t>(const bf16_t* p, int64_t i) { return bf2f(p[i]); }

@@ -27,14 +27,16 @@ template <typename T>
 __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const float* __restrict__ smear_gate,
                                                float smear_lambda, float r0, float a0,
                                                const int* __restrict__ tokens, const int* __restrict__ row_off,
-                                               const int* __restrict__ start, int D, int cap,
+                                               const int* __restrict__ start, int max_per_row, int Mcap, int D,
+                                               int cap,
                                                float* __restrict__ hist, float* __restrict__ x,
                                                float* __restrict__ x0, int* __restrict__ tok_row,
                                                int* __restrict__ tok_pos) {
   __shared__ float sg[EMBED_MAXW], sinv[EMBED_MAXW];
   const int b = blockIdx.x;
-  const int base = row_off[b], n = min(row_off[b + 1] - base, EMBED_MAXW), s0 = start[b];
-  if (n <= 0) return;
+  const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
+  const int base = sp.base, n = sp.n, s0 = start[b];
+  if (n <= 0 || s0 < 0) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int j = threadIdx.x; j < n; j += blockDim.x) {
     tok_row[base + j] = b;
@@ -267,11 +269,11 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   if (dt == FC_BF16)
     hipLaunchKernelGGL(k_embed<bf16_t>, dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
-                       ch->start, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
+                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
   else
     hipLaunchKernelGGL(k_embed<float>, dim3(B), dim3(256), 0, s, (const float*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
-                       ch->start, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
+                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
   FC_LAUNCH_CHECK();
 
   Pending pend{};
@@ -301,8 +303,8 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     int max_keys = c->cap;
     if (L.window > 0) max_keys = std::min(c->cap, L.window + ch->max_per_row);
     rc = fc_launch_attention(w.q, (const char*)c->k + layer_elems * l * es, (const char*)c->v + layer_elems * l * es,
-                             w.y, B, ch->max_per_row, typ_per_row, H, G, hd, c->cap, ch->row_off, ch->start, L.window,
-                             max_keys, dt, w.part, w.part_bytes, s);
+                             w.y, B, Mcap, ch->max_per_row, typ_per_row, H, G, hd, c->cap, ch->row_off, ch->start,
+                             L.window, max_keys, dt, w.part, w.part_bytes, s);
     if (rc) return rc;
     e = Epi{};
     e.mode = EPI_ADD;

@@ -42,9 +42,10 @@ struct AttnGrid {
 };
 AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, int n_kv_head, int max_keys);
 int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head, int head_dim, int max_keys);
-int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_per_row,
-                        int typ_per_row, int H, int G, int hd, int cap, const int* row_off, const int* start,
-                        int window, int max_keys, int dtype, void* part, int64_t part_bytes, hipStream_t s);
+int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_tokens,
+                        int max_per_row, int typ_per_row, int H, int G, int hd, int cap, const int* row_off,
+                        const int* start, int window, int max_keys, int dtype, void* part, int64_t part_bytes,
+                        hipStream_t s);
 int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const fc_model* m, int layer,
                        const fc_cache* c, const int* tok_row, const int* tok_pos, int Mcap, const int* Mdev, void* q,
                        hipStream_t s);

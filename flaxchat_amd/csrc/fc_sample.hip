@@ -315,8 +315,8 @@ __global__ __launch_bounds__(PLAN_THR) void k_spec_plan(SpecDev s) {
     const int b = b0 + threadIdx.x;
     const bool in = b < B;
     const bool active = in && !s.stall[b] && !row_finished(s, b);
-    const int dn = active ? s.d_pend_n[b] : 0;
-    const int tn = active ? s.t_pend_n[b] : 0;
+    const int dn = active ? min(max(s.d_pend_n[b], 0), P) : 0;
+    const int tn = active ? min(max(s.t_pend_n[b], 0), P) : 0;
     int v[3] = {dn, active ? 1 : 0, active ? tn + K : 0}, tot[3];
     scan3(v, tot, sm);
     if (in) {

@@ -193,15 +193,17 @@ int32_t fc_pack_operand(const void* src, void* dst, int32_t rows, int32_t K, voi
 
 /* Split-KV flash-decode attention over a cache layer (flaxchat/engine.py:128-156):
  * GQA head grouping, causal + inclusive sliding window `pos - j <= window`.
- * q: [tokens][H][hd] dtype, packed (row_off, start as in fc_chunk);
- * y: [tokens][H*hd] dtype (rows past row_off[batch] untouched). */
+ * q: [max_tokens][H][hd] dtype, packed (row_off, start as in fc_chunk);
+ * y: [max_tokens][H*hd] dtype (bf16: fragment order over round16(max_tokens)
+ * rows); rows past row_off[batch] untouched. A row whose tokens run past
+ * max_tokens or number more than max_per_row is treated as empty. */
 int64_t fc_attention_workspace_bytes(int32_t batch, int32_t max_per_row, int32_t n_head, int32_t n_kv_head,
                                      int32_t head_dim, int32_t max_keys);
 int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y,
-                     int32_t batch, int32_t max_per_row, int32_t n_head, int32_t n_kv_head,
-                     int32_t head_dim, int32_t cap, const int32_t* row_off, const int32_t* start,
-                     int32_t window, int32_t max_keys, int32_t dtype, void* work, int64_t work_bytes,
-                     void* stream);
+                     int32_t batch, int32_t max_tokens, int32_t max_per_row, int32_t n_head,
+                     int32_t n_kv_head, int32_t head_dim, int32_t cap, const int32_t* row_off,
+                     const int32_t* start, int32_t window, int32_t max_keys, int32_t dtype, void* work,
+                     int64_t work_bytes, void* stream);
 
 /* Per-row statistics of fp32 logits rows (flaxchat/engine.py:461-476):
  * lax.top_k keep-set (exactly k, lower index first among ties), max and

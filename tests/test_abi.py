@@ -41,7 +41,7 @@ def test_argument_errors_are_status_codes():
     L = _lib.lib()
     rc = L.fc_gemm(None, None, None, 1, 1, 8, 0, 0, None)
     assert rc == -1 and b"null" in L.fc_last_error()
-    rc = L.fc_attention(None, None, None, None, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None, 0, None)
+    rc = L.fc_attention(None, None, None, None, 1, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None, 0, None)
     assert rc == -1
     st = _lib.FcSpecState()
     assert L.fc_spec_accept(ctypes.byref(st), None) == -1

@@ -194,7 +194,7 @@ def test_attention_parity(dtype, B, W, H, G, window, lmax):
     max_keys = min(cap, window + W) if window > 0 else cap
     nb = lib().fc_attention_workspace_bytes(B, W, H, G, d, max_keys)
     ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev())
-    check(lib().fc_attention(qt.data_ptr(), Kt.data_ptr(), Vt.data_ptr(), y.data_ptr(), B, W, H, G, d, cap,
+    check(lib().fc_attention(qt.data_ptr(), Kt.data_ptr(), Vt.data_ptr(), y.data_ptr(), B, tot, W, H, G, d, cap,
                              ro.data_ptr(), st.data_ptr(), window, max_keys, code, ws.data_ptr(), ws.numel(),
                              stream()), "attention")
     torch.cuda.synchronize()
