@@ -18,18 +18,38 @@
 
 #define EMBED_MAXW 1024
 
+// Eight consecutive entries of an embedding row as fp32.
+__device__ __forceinline__ void ld8(const bf16_t* p, float* o) {
+  const uint4 v = *(const uint4*)p;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(w[i] << 16);
+    o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void ld8(const float* p, float* o) {
+  const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void st8(float* p, const float* v) {
+  *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+  *(float4*)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 // Embedding + RMSNorm + smear (flaxchat/engine.py:80-94), one workgroup per
 // row. The smear chain x_t = n_t + g_t * x_{t-1} is sequential in t but
-// elementwise in the model dimension, so each thread walks the row's tokens
-// for its own columns. Also records the row and position of every packed
-// token for the later per-token kernels.
+// elementwise in the model dimension: each thread owns 8 consecutive
+// columns and walks the row's tokens, with the embedding loads of the next
+// four tokens issued ahead of the dependent arithmetic. Also records the row
+// and position of every packed token for the later per-token kernels.
+#define EMBED_AHEAD 4
 template <typename T>
 __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const float* __restrict__ smear_gate,
                                                float smear_lambda, float r0, float a0,
                                                const int* __restrict__ tokens, const int* __restrict__ row_off,
                                                const int* __restrict__ start, int max_per_row, int Mcap, int D,
-                                               int cap,
-                                               float* __restrict__ hist, float* __restrict__ x,
+                                               int cap, float* __restrict__ hist, float* __restrict__ x,
                                                float* __restrict__ x0, int* __restrict__ tok_row,
                                                int* __restrict__ tok_pos) {
   __shared__ float sg[EMBED_MAXW], sinv[EMBED_MAXW];
@@ -42,13 +62,15 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
     tok_row[base + j] = b;
     tok_pos[base + j] = s0 + j;
   }
+  // per token: 1 / rms of the embedding row and the smear gate
   for (int j = wave; j < n; j += 4) {
-    const int tok = tokens[base + j];
-    const T* e = wte + (int64_t)tok * D;
+    const T* e = wte + (int64_t)tokens[base + j] * D;
     float ss = 0.f;
-    for (int d = lane; d < D; d += 64) {
-      const float v = ld<T>(e, d);
-      ss += v * v;
+    for (int d = lane * 8; d < D; d += 64 * 8) {
+      float v[8];
+      ld8(e + d, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
     }
     ss = wave_sum(ss);
     const float inv = 1.f / sqrtf(ss / (float)D + 1e-6f);
@@ -59,18 +81,37 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float prev = s0 > 0 ? hist[((int64_t)b * cap + s0 - 1) * D + d] : 0.f;
-    for (int j = 0; j < n; ++j) {
-      const int tok = tokens[base + j];
-      const float nv = ld<T>(wte, (int64_t)tok * D + d) * sinv[j];
-      const float xv = nv + sg[j] * prev;
-      const int pos = s0 + j;
-      if (pos < cap) hist[((int64_t)b * cap + pos) * D + d] = xv;
-      const int64_t m = base + j;
-      x0[m * D + d] = xv;
-      x[m * D + d] = r0 * xv + a0 * xv;
-      prev = xv;
+  for (int c0 = threadIdx.x * 8; c0 < D; c0 += blockDim.x * 8) {
+    float prev[8];
+    if (s0 > 0) ld8(hist + ((int64_t)b * cap + s0 - 1) * D + c0, prev);
+    else
+#pragma unroll
+      for (int i = 0; i < 8; ++i) prev[i] = 0.f;
+    for (int j0 = 0; j0 < n; j0 += EMBED_AHEAD) {
+      float ev[EMBED_AHEAD][8];
+#pragma unroll
+      for (int u = 0; u < EMBED_AHEAD; ++u) {
+        const int j = min(j0 + u, n - 1);
+        ld8(wte + (int64_t)tokens[base + j] * D + c0, ev[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < EMBED_AHEAD; ++u) {
+        const int j = j0 + u;
+        if (j < n) {
+          float xv[8], xr[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xv[i] = ev[u][i] * sinv[j] + sg[j] * prev[i];
+            xr[i] = r0 * xv[i] + a0 * xv[i];
+            prev[i] = xv[i];
+          }
+          const int pos = s0 + j;
+          if (pos < cap) st8(hist + ((int64_t)b * cap + pos) * D + c0, xv);
+          const int64_t m = base + j;
+          st8(x0 + m * D + c0, xv);
+          st8(x + m * D + c0, xr);
+        }
+      }
     }
   }
 }
