@@ -8,12 +8,13 @@
 // (engine.py:164-166) and the 15*tanh(z/15) softcap (engine.py:173-174).
 //
 // Kernels:
-//   k_gemv     VALU dot products: fp32 weights (parity mode), or bf16 with
-//              fewer than 8 rows, where a 16-row matrix-core tile would be
-//              mostly empty.
-//   k_gemm_ks  bf16 MFMA 16x16x32 for everything else (draft steps, verify,
-//              prefill, lm_head): workgroup tile of 16-64 rows x 16-64
-//              columns, the four waves split K, deep register prefetch.
+//   k_gemv     VALU dot products (fp32 weights: the parity mode).
+//   k_gemm_ks  bf16 MFMA 16x16x32, workgroup tile of 16-64 rows x 16-64
+//              columns, the four waves split K, register pipeline; draft
+//              steps and the split-K residual GEMMs.
+//   k_gemm_la  bf16 MFMA, 32-128 rows x 128 columns, the four waves split
+//              the columns and share the activation tile through LDS;
+//              verify / prefill row counts and the verify lm_head.
 // The row count may be a device value (packed token chunks whose size is
 // only known on the GPU): the grid covers the capacity and tiles past the
 // actual count exit at once.
@@ -293,6 +294,131 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
   }
 }
 
+// bf16 MFMA GEMM for larger row counts, A shared through LDS.
+//
+// A workgroup owns an MT x NT tile (MT = 16 MB rows, NT = 64 NBW columns);
+// its four waves split the columns (each 16 NBW of them, all MT rows), so
+// each wave streams only its own weight fragments, straight into registers,
+// while the activation tile of a 64-wide k chunk (2 MB blocks of 1 KB in
+// fragment order) is fetched once per workgroup and shared in LDS. Per
+// output this moves (MT + NT) / (MT NT) of the operand bytes through L2,
+// half of what the K-split kernel's 32 x 64 tile moves at MT = 64, NT = 128.
+// Both operands are loaded NS chunks ahead in a register ring; the A chunk
+// is written to the LDS double buffer one chunk before it is used.
+// Grid and tile order as in k_gemm_ks.
+template <int MB, int NBW, int NS, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                 int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
+                                                 int S, int mtiles, int mfast, Epi e) {
+  static_assert(MB == 2 || MB == 4 || MB == 8, "MB in {2, 4, 8}");
+  constexpr int MT = 16 * MB, NT = 64 * NBW, AB = 2 * MB / 4;  // A blocks per wave per chunk
+  __shared__ uint4 As[2][2 * MB][64];
+  const int id = blockIdx.x;
+  const int ntiles8 = (ntiles + 7) & ~7;
+  int nt, s, mt;
+  if (mfast) {
+    const int xcd = id & 7, loc = id >> 3, per = S * mtiles;
+    const int nl = loc / per, rem = loc - nl * per;
+    s = rem / mtiles;
+    mt = rem - s * mtiles;
+    nt = nl * 8 + xcd;
+  } else {
+    nt = id % ntiles8;
+    const int rest = id / ntiles8;
+    s = rest % S;
+    mt = rest / S;
+  }
+  if (nt >= ntiles) return;
+  const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
+  const int m0 = mt * MT;
+  if (m0 >= M) return;
+  const int n0 = nt * NT;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int C = K >> 6;
+  const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
+  const int n = c_end - c_beg;
+  const int64_t KS32 = K >> 5;
+  // this wave's A blocks of a chunk: q = wave + 4 u, row block q / 2, k step q % 2
+  const int last_blk = (M - 1) >> 4;
+  const bf16_t* abase[AB];
+#pragma unroll
+  for (int u = 0; u < AB; ++u) {
+    const int q = wave + 4 * u;
+    abase[u] = A + ((int64_t)min(m0 / 16 + q / 2, last_blk) * KS32 + (q & 1)) * 512 + lane * 8;
+  }
+  const bf16_t* wbase[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) wbase[j] = W + (int64_t)(n0 / 16 + wave * NBW + j) * KS32 * 512 + lane * 8;
+
+  f32x4 acc[MB][NBW];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (n > 0) {
+    v4u wr[NS][NBW][2], ar[NS][AB];
+#define LA_LOAD(slot, i)                                                              \
+  {                                                                                   \
+    const int c_ = c_beg + min((i), n - 1);                                           \
+    _Pragma("unroll") for (int j = 0; j < NBW; ++j)                                   \
+      _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                                \
+        wr[slot][j][ks] = *(const v4u*)(wbase[j] + (2 * c_ + ks) * 512);              \
+    _Pragma("unroll") for (int u = 0; u < AB; ++u)                                    \
+      ar[slot][u] = *(const v4u*)(abase[u] + (int64_t)c_ * 1024);                     \
+  }
+#define LA_STAGE_A(slot, buf)                                                         \
+  {                                                                                   \
+    _Pragma("unroll") for (int u = 0; u < AB; ++u)                                    \
+      As[buf][wave + 4 * u][lane] = __builtin_bit_cast(uint4, ar[slot][u]);           \
+  }
+#pragma unroll
+    for (int p = 0; p < NS; ++p) LA_LOAD(p, p);
+    LA_STAGE_A(0, 0);
+    __syncthreads();
+    for (int i0 = 0; i0 < n; i0 += NS) {
+#pragma unroll
+      for (int p = 0; p < NS; ++p) {
+        const int i = i0 + p;
+        const int buf = i & 1;
+        if (i < n) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+              const v4u a = __builtin_bit_cast(v4u, As[buf][2 * mb + ks][lane]);
+#pragma unroll
+              for (int j = 0; j < NBW; ++j) acc[mb][j] = mfma16(a, wr[p][j][ks], acc[mb][j]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // next chunk's A into the other LDS buffer (its last reader was
+        // chunk i - 1, finished before the previous barrier), then refill
+        // the freed ring slots
+        LA_STAGE_A((p + 1) % NS, buf ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        LA_LOAD(p, i + NS);
+        __syncthreads();
+      }
+    }
+#undef LA_LOAD
+#undef LA_STAGE_A
+  }
+
+  Epi ee = e;
+  ee.split = s;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mb + 4 * g + i;
+        if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i]);
+      }
+}
+
 // ---------------------------------------------------------------------------
 // Dispatch
 // ---------------------------------------------------------------------------
@@ -334,12 +460,24 @@ static void launch_ks(const void* A, const void* W, int Mcap, const int* Mdev, i
                                            mfast, e));
 }
 
+#define FC_GEMM_LA_NS 3
+template <int MB, int NBW>
+static void launch_la(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int S, const Epi& e,
+                      hipStream_t s) {
+  const int ntiles = N / (64 * NBW), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
+  const int nwg = (ntiles + 7) / 8 * 8 * S * mtiles;
+  const int mfast = Mdev == nullptr ? 1 : 0;
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_la<MB, NBW, FC_GEMM_LA_NS, E>), dim3(nwg), dim3(256), 0, s,
+                                           (const bf16_t*)A, (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, S, mtiles,
+                                           mfast, e));
+}
+
 // One plan drives the workspace sizing and the launch. The tile shape and
 // the K split are chosen for the typical row count Mtyp (the grid covers
 // Mcap rows; tiles past the device-side count exit at once).
 struct GemmPlan {
-  bool gemv;
-  int mb, nb, S;
+  bool gemv, la;  // VALU GEMV (fp32) / LDS-shared-A kernel (else the K-split kernel)
+  int mb, nb, S;  // k_gemm_ks: 16 mb x 16 nb tile; k_gemm_la: 16 mb x 64 nb tile
 };
 // Tile shape and K split by typical row count, from sweeps on MI355X at the
 // engine's shapes (N = 1536 / 4608 / 6144 / 65536, K = 1536 / 6144).
@@ -366,6 +504,13 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     p.mb = 4;
     p.nb = 4;
     p.S = std::min(2, s_max);
+  } else if (!can_split && Mtyp >= 128 && N % 128 == 0) {
+    // verify / prefill rows: A shared through LDS, 128-column tiles; a wide
+    // output (lm_head) also takes 128-row tiles
+    p.la = true;
+    p.mb = N >= 16384 ? 8 : 2;
+    p.nb = 2;
+    return p;
   } else {
     p.mb = 2;
     p.nb = 4;
@@ -402,6 +547,9 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   }
   if (p.gemv) {
     launch_gemv<float>(A, W, Mcap, Mdev, N, K, ee, s);
+  } else if (p.la) {
+    if (p.mb == 8) launch_la<8, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+    else launch_la<2, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
   } else if (p.mb == 1) {
     if (p.nb == 4) launch_ks<1, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
     else launch_ks<1, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
