@@ -30,6 +30,17 @@
 #ifndef FC_ATTN_PIPE
 #define FC_ATTN_PIPE 0
 #endif
+// K/V cache loads are streamed once per call: non-temporal loads keep them
+// from displacing reusable lines in the caches (measured ~8% faster at cfg4)
+#ifndef FC_ATTN_NT
+#define FC_ATTN_NT 1
+#endif
+#if FC_ATTN_NT
+typedef uint32_t kv_u32x4 __attribute__((ext_vector_type(4)));
+#define KV_LD(p) __builtin_bit_cast(uint4, __builtin_nontemporal_load((const kv_u32x4*)(p)))
+#else
+#define KV_LD(p) (*(p))
+#endif
 
 // K cache of the matrix-core path (bf16, head_dim 128): 32-key blocks of
 // 8 KB in the fragment order of the S^T = K Q^T product. In a block, load
@@ -274,9 +285,9 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
   {                                                                                                \
     const bf16_t* kt = kbase + (int64_t)((kb_) >> 5) * 32 * HD + lane * 8;                         \
     _Pragma("unroll") for (int cc = 0; cc < 2; ++cc)                                               \
-      _Pragma("unroll") for (int s = 0; s < 4; ++s) kf[cc][s] = *(const uint4*)(kt + (s * 2 + cc) * 512); \
+      _Pragma("unroll") for (int s = 0; s < 4; ++s) kf[cc][s] = KV_LD((const uint4*)(kt + (s * 2 + cc) * 512)); \
     const bf16_t* vt = vbase + (int64_t)((kb_) >> 5) * HD * 32 + r * 32 + 8 * g4;                  \
-    _Pragma("unroll") for (int db = 0; db < 8; ++db) vf[db] = *(const uint4*)(vt + db * 16 * 32);  \
+    _Pragma("unroll") for (int db = 0; db < 8; ++db) vf[db] = KV_LD((const uint4*)(vt + db * 16 * 32));  \
   }
 #if FC_ATTN_PIPE
   // two tiles in flight per wave: the next tile's loads are issued before the
