@@ -51,11 +51,11 @@ CONFIGS = {
                   window_pattern="SSSL", short_window=2048), 4, 128, 6144, 1024, 8, 0.0, 3),
 }
 HBM_PEAK_GBS = 8000.0
-# HBM bytes / algorithmic bytes of the verify attention (k_attn_mfma +
-# k_attn_combine), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
-# `bench.py --roofline-only`, each scaled by the counter's reading for a
+# HBM bytes / algorithmic bytes of the verify attention (k_attn_mfma, one key
+# split, no combine), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes
+# over `bench.py --roofline-only`, each scaled by the counter's reading for a
 # 256 MiB copy (FETCH_SIZE x2.0, WRITE_SIZE x1.0); see profiles/.
-ATTN_TRAFFIC_RATIO = 1.14
+ATTN_TRAFFIC_RATIO = 1.02
 
 
 def attention_roofline(sess, n_rep=3):
@@ -125,6 +125,47 @@ def attention_roofline(sess, n_rep=3):
                 S=res["S"], L=res["L"], nS=nS, nL=nL)
 
 
+def gemm_calibration(n_iter=20, n_copies=4):
+    """fc_gemm (fragment-order operands, store epilogue) against torch.matmul
+    (hipBLASLt) on the cfg4 engine's GEMM shapes; `n_copies` weight copies are
+    cycled so no launch finds its weights in the Infinity Cache."""
+    import torch
+    from flaxchat_amd import _lib
+    from flaxchat_amd.runtime import pack_operand
+    dev = torch.device("cuda", torch.cuda.current_device())
+    s = torch.cuda.current_stream()
+    out = []
+    for (label, M, N, K) in [("draft c_q|c_k|c_v", 32, 4608, 1536), ("draft c_fc", 32, 6144, 1536),
+                             ("draft c_proj (mlp)", 32, 1536, 6144), ("draft lm_head", 32, 65536, 1536),
+                             ("verify c_q|c_k|c_v", 224, 4608, 1536), ("verify c_fc", 224, 6144, 1536),
+                             ("verify c_proj (mlp)", 224, 1536, 6144), ("verify lm_head", 224, 65536, 1536)]:
+        A = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        Ws = [torch.randn(N, K, device=dev).mul_(0.02).to(torch.bfloat16) for _ in range(n_copies)]
+        Ap = pack_operand(A) if M % 32 == 0 else None
+        Wps = [pack_operand(w) for w in Ws]
+        C = torch.empty(M, N, device=dev)
+        torch.cuda.synchronize()
+
+        def t_of(fn):
+            for i in range(n_copies):
+                fn(i)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(n_iter):
+                fn(i % n_copies)
+            e1.record(s)
+            e1.synchronize()
+            return e0.elapsed_time(e1) / n_iter * 1e3
+
+        ours = t_of(lambda i: _lib.check(_lib.lib().fc_gemm(Ap.data_ptr(), Wps[i].data_ptr(), C.data_ptr(), M, N, K,
+                                                            _lib.FC_BF16, 0, s.cuda_stream), "fc_gemm"))
+        blas = t_of(lambda i: torch.matmul(A, Ws[i].t()))
+        out.append(dict(gemm=label, M=M, N=N, K=K, weight_mb=round(N * K * 2 / 1e6, 1), fc_gemm_us=round(ours, 1),
+                        hipblaslt_us=round(blas, 1)))
+        del Ws, Wps
+    return out
+
+
 def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0):
     """The oracle's literal-mode generate_speculative on host cores."""
     from flaxchat_amd.runtime import to_host
@@ -160,6 +201,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--gemm-calibration", action="store_true",
+                    help="time fc_gemm against torch.matmul (hipBLASLt) on the cfg4 GEMM shapes and exit")
     ap.add_argument("--roofline-only", action="store_true",
                     help="prefill + warmup rounds, then only the verify-attention timing and a 256 MiB copy "
                          "(the counter-calibration kernel); for rocprofv3 --pmc passes")
@@ -174,6 +217,11 @@ def main():
     from flaxchat_amd.config import GPTConfig
     from flaxchat_amd.engine import SpecSession
     from flaxchat_amd.runtime import DeviceModel
+
+    if args.gemm_calibration:
+        for row in gemm_calibration():
+            print(json.dumps(row), flush=True)
+        return
 
     tk, n_draft, B, P, new, k, temp, seed = CONFIGS[args.config]
     cfg = GPTConfig(**tk)
@@ -220,7 +268,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
-                "kernel": "k_attn_mfma + k_attn_combine (verify, k+1 queries per row)",
+                "kernel": "k_attn_mfma (verify, k+1 queries per row, one key split)",
                 "per_launch_bytes": int(r["per_launch_bytes"]), "per_launch_us": round(r["per_launch_us"], 2),
                 "S_layer": r["S"], "L_layer": r["L"]}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s", file=sys.stderr, flush=True)

@@ -137,6 +137,15 @@ __global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* 
 // 32-wide k step; the f32x4 result holds rows 4*(l/16)+i of column l % 16.
 // ---------------------------------------------------------------------------
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+// weight fragment loads (non-temporal when FC_GEMM_W_NT)
+#ifndef FC_GEMM_W_NT
+#define FC_GEMM_W_NT 0
+#endif
+#if FC_GEMM_W_NT
+#define W_LD(p) __builtin_nontemporal_load(p)
+#else
+#define W_LD(p) (*(p))
+#endif
 __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                   0, 0);
@@ -236,7 +245,7 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
     const int c_ = c_beg + wave + 4 * min((i), nch - 1);                            \
     _Pragma("unroll") for (int j = 0; j < NB; ++j)                                  \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
-        wb[j][ks] = *(const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems);           \
+        wb[j][ks] = W_LD((const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems));      \
     _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                               \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
         ab[mb][ks] = *(const v4u*)(arow[mb] + (2 * c_ + ks) * kstep_elems);         \
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
     const int c_ = c_beg + min((i), n - 1);                                           \
     _Pragma("unroll") for (int j = 0; j < NBW; ++j)                                   \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                                \
-        wr[slot][j][ks] = *(const v4u*)(wbase[j] + (2 * c_ + ks) * 512);              \
+        wr[slot][j][ks] = W_LD((const v4u*)(wbase[j] + (2 * c_ + ks) * 512));         \
     _Pragma("unroll") for (int u = 0; u < AB; ++u)                                    \
       ar[slot][u] = *(const v4u*)(abase[u] + (int64_t)c_ * 1024);                     \
   }
