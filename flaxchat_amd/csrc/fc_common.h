@@ -37,6 +37,19 @@ template <> __device__ __forceinline__ int64_t act_idx<uint16_t>(int64_t r, int 
 template <> __device__ __forceinline__ int64_t act_idx<float>(int64_t r, int k, int K) { return r * K + k; }
 __host__ __device__ __forceinline__ int64_t round16(int64_t r) { return (r + 15) / 16 * 16; }
 
+// K cache of the matrix-core path (bf16, head_dim 128): 32-key blocks of
+// 8 KB in the fragment order of the S^T = K Q^T product. In a block, load
+// (cc, s) of lane l = r + 16 g (1 KB contiguous) holds key
+// 8 (r / 4) + r % 4 + 4 cc, dims 32 s + 8 g .. +7; so element (key kk of
+// the block, dim d) sits at ((2 s + cc) 64 + r + 16 g) 8 + d % 8 with
+// s = d / 32, g = (d / 8) % 4, r = 4 (kk / 8) + kk % 4, cc = (kk / 4) % 2.
+__device__ __forceinline__ int64_t kblk_idx(int pos, int d) {
+  const int kk = pos & 31;
+  const int r = ((kk >> 3) << 2) | (kk & 3), cc = (kk >> 2) & 1;
+  const int s = d >> 5, g = (d >> 3) & 3;
+  return (int64_t)(pos >> 5) * 4096 + ((((s << 1) | cc) << 6) + r + (g << 4)) * 8 + (d & 7);
+}
+
 // Packed tokens of row b (row_off as in fc_chunk): n = 0 when the descriptor
 // is out of range (more than max_per_row tokens, or past the capacity), so a
 // bad descriptor feeds nothing instead of addressing outside the buffers.

@@ -306,6 +306,7 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   const int64_t layer_elems = (int64_t)B * G * c->cap * hd;
   const int es = dt == FC_BF16 ? 2 : 4;
   const int typ_per_row = std::max(1, (Mtyp + B - 1) / B);
+  const bool fuse_qkv = fc_gemm_fuses_qkv(Mtyp, NQKV, D, dt, hd);
 
   if (dt == FC_BF16)
     hipLaunchKernelGGL(k_embed<bf16_t>, dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
@@ -334,13 +335,37 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     norm(Mcap, 0);
     FC_LAUNCH_CHECK();
     Epi e{};
-    e.mode = EPI_STORE;
-    e.out = w.qkv;
-    e.ldo = NQKV;
-    rc = fc_launch_gemm(w.h, L.wqkv, Mcap, Mdev, Mtyp, NQKV, D, dt, e, w.gw, s, nullptr);
-    if (rc) return rc;
-    rc = fc_launch_prologue(w.qkv, w.h, ch->tokens, m, l, c, w.tok_row, w.tok_pos, Mcap, Mdev, w.q, s);
-    if (rc) return rc;
+    if (fuse_qkv) {  // the QKV GEMM finishes RoPE / QK-norm / VE gate / KV append itself
+      e.mode = EPI_QKV;
+      QkvEpi& Q = e.qkv;
+      Q.tokens = ch->tokens;
+      Q.tok_row = w.tok_row;
+      Q.tok_pos = w.tok_pos;
+      Q.rcos = m->rope_cos;
+      Q.rsin = m->rope_sin;
+      Q.rope_len = m->rope_len;
+      Q.ve = (const uint16_t*)L.ve;
+      Q.ve_gate = L.ve_gate;
+      Q.h = (const uint16_t*)w.h;
+      Q.D = D;
+      Q.H = H;
+      Q.G = G;
+      Q.B = B;
+      Q.cap = c->cap;
+      Q.kc = (uint16_t*)c->k + layer_elems * l;
+      Q.vc = (uint16_t*)c->v + layer_elems * l;
+      Q.q = (uint16_t*)w.q;
+      rc = fc_launch_gemm(w.h, L.wqkv, Mcap, Mdev, Mtyp, NQKV, D, dt, e, w.gw, s, nullptr);
+      if (rc) return rc;
+    } else {
+      e.mode = EPI_STORE;
+      e.out = w.qkv;
+      e.ldo = NQKV;
+      rc = fc_launch_gemm(w.h, L.wqkv, Mcap, Mdev, Mtyp, NQKV, D, dt, e, w.gw, s, nullptr);
+      if (rc) return rc;
+      rc = fc_launch_prologue(w.qkv, w.h, ch->tokens, m, l, c, w.tok_row, w.tok_pos, Mcap, Mdev, w.q, s);
+      if (rc) return rc;
+    }
     int max_keys = c->cap;
     if (L.window > 0) max_keys = std::min(c->cap, L.window + ch->max_per_row);
     rc = fc_launch_attention(w.q, (const char*)c->k + layer_elems * l * es, (const char*)c->v + layer_elems * l * es,

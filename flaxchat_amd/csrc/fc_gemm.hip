@@ -303,6 +303,86 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
   }
 }
 
+// Attention prologue of one token and one head slot from its fp32 GEMM
+// output row x (128 values; flaxchat/engine.py:96-126, flaxchat/gpt.py:65-71):
+// q / k heads get RoPE (pairs d, d + 64) and 1.2 * RMSNorm, v heads the
+// value-embedding gate; q goes to q[m][head], k / v to the cache at the
+// token's position. Eight consecutive lanes share a token (`part` = which
+// 8 rotary pairs); all 8 take part in the norm's shuffles.
+__device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int m, int M, int hh, int part) {
+  const bool live = m < M;
+  float x1[8], x2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x1[e] = x[8 * part + e];
+    x2[e] = x[64 + 8 * part + e];
+  }
+  int b = 0, pos = 0;
+  if (live) {
+    b = Q.tok_row[m];
+    pos = Q.tok_pos[m];
+  }
+  const bool in_cache = live && (unsigned)b < (unsigned)Q.B && pos >= 0 && pos < Q.cap;
+  if (hh < Q.H + Q.G) {
+    const int pc = min(max(pos, 0), Q.rope_len - 1);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float c = Q.rcos[(int64_t)pc * 64 + 8 * part + e], s = Q.rsin[(int64_t)pc * 64 + 8 * part + e];
+      const float y1 = x1[e] * c + x2[e] * s;
+      const float y2 = x1[e] * (-s) + x2[e] * c;
+      x1[e] = y1;
+      x2[e] = y2;
+      ss += y1 * y1 + y2 * y2;
+    }
+    ss += __shfl_xor(ss, 1, WAVE);
+    ss += __shfl_xor(ss, 2, WAVE);
+    ss += __shfl_xor(ss, 4, WAVE);
+    const float inv = 1.f / sqrtf(ss / 128.f + 1e-6f);
+    uint4 p1, p2;
+    uint32_t* w1 = (uint32_t*)&p1;
+    uint32_t* w2 = (uint32_t*)&p2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w1[e] = (uint32_t)f2bf(x1[2 * e] * inv * 1.2f) | ((uint32_t)f2bf(x1[2 * e + 1] * inv * 1.2f) << 16);
+      w2[e] = (uint32_t)f2bf(x2[2 * e] * inv * 1.2f) | ((uint32_t)f2bf(x2[2 * e + 1] * inv * 1.2f) << 16);
+    }
+    if (hh < Q.H) {
+      if (live) {
+        bf16_t* qo = Q.q + ((int64_t)m * Q.H + hh) * 128;
+        *(uint4*)(qo + 8 * part) = p1;
+        *(uint4*)(qo + 64 + 8 * part) = p2;
+      }
+    } else if (in_cache) {
+      bf16_t* kg = Q.kc + ((int64_t)b * Q.G + (hh - Q.H)) * Q.cap * 128;
+      *(uint4*)(kg + kblk_idx(pos, 8 * part)) = p1;       // 8 consecutive dims stay contiguous
+      *(uint4*)(kg + kblk_idx(pos, 64 + 8 * part)) = p2;
+    }
+  } else {
+    const int gv = hh - Q.H - Q.G;
+    if (Q.ve != nullptr && live) {
+      float z = 0.f;
+#pragma unroll
+      for (int i = 0; i < 12; ++i) z += bf2f(Q.h[frag_idx(m, i, Q.D)]) * Q.ve_gate[gv * 12 + i];
+      const float gate = 3.f * (1.f / (1.f + expf(-z)));
+      const bf16_t* vr = Q.ve + ((int64_t)Q.tokens[m] * Q.G + gv) * 128;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x1[e] = x1[e] + gate * bf2f(vr[8 * part + e]);
+        x2[e] = x2[e] + gate * bf2f(vr[64 + 8 * part + e]);
+      }
+    }
+    if (in_cache) {
+      bf16_t* vb = Q.vc + (((int64_t)b * Q.G + gv) * (Q.cap / 32) + pos / 32) * 128 * 32 + (pos & 31);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vb[(8 * part + e) * 32] = f2bf(x1[e]);
+        vb[(64 + 8 * part + e) * 32] = f2bf(x2[e]);
+      }
+    }
+  }
+}
+
 // bf16 MFMA GEMM for larger row counts, A shared through LDS.
 //
 // A workgroup owns an MT x NT tile (MT = 16 MB rows, NT = 64 NBW columns);
@@ -415,17 +495,33 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #undef LA_STAGE_A
   }
 
-  Epi ee = e;
-  ee.split = s;
+  if constexpr (EPI == EPI_QKV) {
+    // the tile is one head (column tile nt = head slot) for 32 tokens: stage
+    // it in LDS, then 8 threads per token finish it (16 dims each: d and
+    // d + 64 of 8 rotary pairs)
+    static_assert(MB == 2 && NBW == 2, "EPI_QKV needs 32 x 128 tiles");
+    __shared__ float T[32][128 + 4];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int j = 0; j < NBW; ++j)
+      for (int j = 0; j < NBW; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 16 * mb + 4 * g + i;
-        if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i]);
-      }
+        for (int i = 0; i < 4; ++i) T[16 * mb + 4 * g + i][16 * (wave * NBW + j) + r] = acc[mb][j][i];
+    __syncthreads();
+    qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7);
+  } else {
+    Epi ee = e;
+    ee.split = s;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + 16 * mb + 4 * g + i;
+          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i]);
+        }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -481,6 +577,14 @@ static void launch_la(const void* A, const void* W, int Mcap, const int* Mdev, i
                                            mfast, e));
 }
 
+static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
+                          hipStream_t s) {
+  const int ntiles = N / 128, mtiles = (Mcap + 31) / 32;
+  const int nwg = (ntiles + 7) / 8 * 8 * mtiles;
+  hipLaunchKernelGGL((k_gemm_la<2, 2, FC_GEMM_LA_NS, EPI_QKV>), dim3(nwg), dim3(256), 0, s, (const bf16_t*)A,
+                     (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, 1, mtiles, Mdev == nullptr ? 1 : 0, e);
+}
+
 // One plan drives the workspace sizing and the launch. The tile shape and
 // the K split are chosen for the typical row count Mtyp (the grid covers
 // Mcap rows; tiles past the device-side count exit at once).
@@ -529,6 +633,12 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
   return p;
 }
 
+bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
+  if (dtype != FC_BF16 || head_dim != 128 || N % 128 != 0 || K % 64 != 0) return false;
+  const GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
+  return p.la && p.mb == 2 && p.nb == 2;
+}
+
 int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K) {
   if (Mtyp <= 0 || Mcap <= 0 || N <= 0 || K <= 0) return 0;
   GemmPlan p = plan_gemm(Mtyp, N, K, FC_BF16, true);
@@ -543,6 +653,12 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   if (Mtyp <= 0 || Mtyp > Mcap) Mtyp = Mcap;
   FC_CHECK_ARG(dtype == FC_F32 || (K % 64 == 0 && N % 32 == 0),
                "bf16 GEMM needs K % 64 == 0 and N % 32 == 0 (fragment-order operands)");
+  if (e.mode == EPI_QKV) {
+    FC_CHECK_ARG(fc_gemm_fuses_qkv(Mtyp, N, K, dtype, 128), "EPI_QKV needs the 32 x 128 bf16 tile");
+    launch_la_qkv(A, W, Mcap, Mdev, N, K, e, s);
+    FC_LAUNCH_CHECK();
+    return FC_OK;
+  }
   const bool can_split = splits != nullptr && gw.part != nullptr;
   GemmPlan p = plan_gemm(Mtyp, N, K, dtype, can_split);
   if (p.S > 1 && (int64_t)p.S * Mcap * N * 4 > gw.part_bytes) p.S = 1;

@@ -3,7 +3,22 @@
 #include "fc_common.h"
 #include <algorithm>
 
-enum { EPI_STORE = 0, EPI_ADD = 1, EPI_RELU2 = 2, EPI_MLPOUT = 3, EPI_SOFTCAP = 4, EPI_PARTIAL = 5 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_RELU2 = 2, EPI_MLPOUT = 3, EPI_SOFTCAP = 4, EPI_PARTIAL = 5, EPI_QKV = 6 };
+
+// EPI_QKV: the c_q|c_k|c_v GEMM finishes each (token, head) itself: RoPE +
+// 1.2 RMSNorm for q / k heads, value-embedding gate for v heads, q written
+// [M][H][128] bf16, k / v appended to the layer's cache (what k_prologue
+// does after a plain GEMM).
+struct QkvEpi {
+  const int *tokens, *tok_row, *tok_pos;
+  const float *rcos, *rsin;
+  int rope_len;
+  const uint16_t* ve;     // [Vp][G*128] or NULL
+  const float* ve_gate;   // [G][12]
+  const uint16_t* h;      // the GEMM's A operand (fragment order), for the gate
+  int D, H, G, B, cap;
+  uint16_t *kc, *vc, *q;  // layer's K / V cache, q output
+};
 
 struct Epi {
   int mode;
@@ -22,6 +37,7 @@ struct Epi {
   // EPI_PARTIAL: split `split` writes part[(split * part_rows + m) * ldo + n]
   float* part;
   int part_rows, split;
+  QkvEpi qkv;
 };
 
 #define FC_MAX_SPLIT 8
@@ -33,6 +49,9 @@ struct GemmWork {
 int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K);
 // `splits` (may be NULL: no split) receives the split count; when > 1 the
 // output was written as partials to gw.part and the caller must finish it.
+// true when the GEMM of this shape runs the tile that can finish the
+// attention prologue in its epilogue (EPI_QKV; 128-column tiles, bf16)
+bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim);
 int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int Mtyp, int N, int K, int dtype,
                    const Epi& e, const GemmWork& gw,
                    hipStream_t s, int* splits);

@@ -61,12 +61,18 @@ def test_forward_logits_vs_oracle(which, dtype, tiny_pair, cfg1_pair):
     got = _device_logits(tgt, toks, dtype, [17, 1, 5, 17])
     err = np.abs(got - ref).max()
     if which == "cfg1":
-        # a 70-slot chunk runs the LDS-tiled GEMMs (M > 64), with split-K
-        # partials finished by the RMSNorm kernels
+        # a 70-token chunk runs the 64-row tiles with split-K partials finished
+        # by the RMSNorm kernels; a 130-token chunk runs the LDS-shared tiles
+        # and, in bf16, the QKV GEMM that finishes RoPE / QK-norm / VE / KV
+        # append in its epilogue
         toks2 = rng.integers(0, tgt.config.vocab_size, 80).tolist()
         ref2 = _oracle_logits(tgt, toks2)
         got2 = _device_logits(tgt, toks2, dtype, [70, 3, 7])
         err = max(err, np.abs(got2 - ref2).max())
+        toks3 = rng.integers(0, tgt.config.vocab_size, 140).tolist()
+        ref3 = _oracle_logits(tgt, toks3)
+        got3 = _device_logits(tgt, toks3, dtype, [130, 10])
+        err = max(err, np.abs(got3 - ref3).max())
     _say(f"  max abs err {err:.3e}")
     assert err < (1e-3 if dtype == "fp32" else 5e-2)
 
