@@ -399,7 +399,7 @@ template <int MB, int NBW, int NS, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
                                                  int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
                                                  int S, int mtiles, int mfast, Epi e) {
-  static_assert(MB == 2 || MB == 4 || MB == 8, "MB in {2, 4, 8}");
+  static_assert(MB == 2 || MB == 4 || MB == 8 || MB == 16, "MB in {2, 4, 8, 16}");
   constexpr int MT = 16 * MB, NT = 64 * NBW, AB = 2 * MB / 4;  // A blocks per wave per chunk
   __shared__ uint4 As[2][2 * MB][64];
   const int id = blockIdx.x;
@@ -610,6 +610,12 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     const int wgs = N / 64;
     if (can_split && wgs < 256) p.S = std::min((256 + wgs - 1) / wgs, s_max);
   } else if (Mtyp <= 32) {
+    if (!can_split && N >= 16384 && N % 128 == 0) {  // draft lm_head: LDS-shared rows, 128-column tiles
+      p.la = true;
+      p.mb = 2;
+      p.nb = 2;
+      return p;
+    }
     p.mb = 2;
     p.nb = 2;
     if (can_split) p.S = std::min(K > 2048 ? 4 : 2, s_max);
