@@ -9,7 +9,7 @@
 //
 // Kernels:
 //   k_gemv     VALU dot products (fp32 weights: the parity mode).
-//   k_gemm_ks  bf16 MFMA 16x16x32, workgroup tile of 16-64 rows x 16-64
+//   k_gemm_ks  bf16 MFMA 16x16x32, workgroup tile of 16-32 rows x 16-64
 //              columns, the four waves split K, register pipeline; draft
 //              steps and the split-K residual GEMMs.
 //   k_gemm_la  bf16 MFMA, 32-128 rows x 128 columns, the four waves split
@@ -236,44 +236,46 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
   }
 
   if (nch > 0) {
-    static_assert(NS == 2, "the pipeline below is written for two stages");
-    v4u wb0[NB][2], ab0[MB][2], wb1[NB][2], ab1[MB][2];
+    static_assert(NS >= 2 && NS <= 4, "register ring of 2-4 chunks");
+    v4u wb[NS][NB][2], ab[NS][MB][2];
     // chunk index of the wave's i-th chunk, clamped so the tail loads are
     // harmless re-reads and the loop body has no branch
-#define KS_LOAD(wb, ab, i)                                                          \
+#define KS_LOAD(slot, i)                                                            \
   {                                                                                 \
     const int c_ = c_beg + wave + 4 * min((i), nch - 1);                            \
     _Pragma("unroll") for (int j = 0; j < NB; ++j)                                  \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
-        wb[j][ks] = W_LD((const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems));      \
+        wb[slot][j][ks] = W_LD((const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems)); \
     _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                               \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
-        ab[mb][ks] = *(const v4u*)(arow[mb] + (2 * c_ + ks) * kstep_elems);         \
+        ab[slot][mb][ks] = *(const v4u*)(arow[mb] + (2 * c_ + ks) * kstep_elems);   \
   }
-#define KS_MMA(wb, ab)                                                              \
+#define KS_MMA(slot)                                                                \
   {                                                                                 \
     _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                                \
       _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                             \
         _Pragma("unroll") for (int j = 0; j < NB; ++j)                              \
-          acc[mb][j] = mfma16(ab[mb][ks], wb[j][ks], acc[mb][j]);                   \
+          acc[mb][j] = mfma16(ab[slot][mb][ks], wb[slot][j][ks], acc[mb][j]);       \
   }
-    KS_LOAD(wb0, ab0, 0);
-    KS_LOAD(wb1, ab1, 1);
+#pragma unroll
+    for (int p = 0; p < NS; ++p) KS_LOAD(p, p);
     int i = 0;
     // the scheduling barriers keep each chunk's loads together and after the
-    // MFMAs that free its registers, so the other stage's loads stay in
-    // flight while a stage computes (the waits become vmcnt(one stage))
-    for (; i + 1 < nch; i += 2) {
-      KS_MMA(wb0, ab0);
-      __builtin_amdgcn_sched_barrier(0);
-      KS_LOAD(wb0, ab0, i + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      KS_MMA(wb1, ab1);
-      __builtin_amdgcn_sched_barrier(0);
-      KS_LOAD(wb1, ab1, i + 3);
-      __builtin_amdgcn_sched_barrier(0);
+    // MFMAs that free its registers, so the other slots' loads stay in flight
+    // while a slot computes (the waits become vmcnt(NS - 1 slots))
+    for (; i + NS - 1 < nch; i += NS) {
+#pragma unroll
+      for (int p = 0; p < NS; ++p) {
+        KS_MMA(p);
+        __builtin_amdgcn_sched_barrier(0);
+        KS_LOAD(p, i + NS + p);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    if (i < nch) KS_MMA(wb0, ab0);
+    // the last nch - i < NS chunks sit in slots 0 .. nch - i - 1
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+      if (i + p < nch) KS_MMA(p);
 #undef KS_LOAD
 #undef KS_MMA
   }
@@ -553,14 +555,15 @@ static void launch_gemv(const void* A, const void* W, int M, const int* Mdev, in
   else launch_gemv_mb<T, 8>(A, W, M, Mdev, N, K, e, s);
 }
 
-#define FC_GEMM_NS 2
-template <int MB, int NB, bool PK = false>
+// register ring depth of the K-split kernel: 4 chunks for the 32 x 16 tile
+// (few columns, long weight streams per wave), else 3
+template <int MB, int NB, bool PK = false, int NS = (MB == 2 && NB == 1) ? 4 : 3>
 static void launch_ks(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int S, const Epi& e,
                       hipStream_t s) {
   const int ntiles = N / (16 * NB), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
   const int nwg = (ntiles + 7) / 8 * 8 * S * mtiles;
   const int mfast = Mdev == nullptr ? 1 : 0;
-  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_ks<MB, NB, FC_GEMM_NS, E, PK>), dim3(nwg), dim3(256), 0, s,
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_ks<MB, NB, NS, E, PK>), dim3(nwg), dim3(256), 0, s,
                                            (const bf16_t*)A, (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, S, mtiles,
                                            mfast, e));
 }
@@ -618,12 +621,15 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     }
     p.mb = 2;
     p.nb = 2;
-    if (can_split) p.S = std::min(K > 2048 ? 4 : 2, s_max);
-  } else if (can_split && K > 2048) {
-    p.mb = 4;
+    if (can_split) {  // n_embd columns: 16-column tiles and a K split fill the GPU
+      p.nb = 1;
+      p.S = std::min(K > 2048 ? 8 : 3, s_max);
+    }
+  } else if (can_split) {
+    p.mb = 2;
     p.nb = 4;
-    p.S = std::min(2, s_max);
-  } else if (!can_split && Mtyp >= 128 && N % 128 == 0) {
+    p.S = std::min(3, s_max);
+  } else if (Mtyp >= 128 && N % 128 == 0) {
     // verify / prefill rows: A shared through LDS, 128-column tiles; a wide
     // output (lm_head) also takes 128-row tiles
     p.la = true;
@@ -635,7 +641,7 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     p.nb = 4;
   }
   while (p.nb > 1 && N % (16 * p.nb) != 0) p.nb /= 2;
-  if (p.nb == 1 && p.mb != 2) p.nb = 2;  // instantiated shapes: (1,2|4), (2,1|2|4), (4,2|4)
+  if (p.nb == 1 && p.mb != 2) p.nb = 2;  // instantiated shapes: (1,2|4), (2,1|2|4)
   return p;
 }
 
@@ -684,13 +690,10 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   } else if (p.mb == 1) {
     if (p.nb == 4) launch_ks<1, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
     else launch_ks<1, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
-  } else if (p.mb == 2) {
+  } else {
     if (p.nb == 4) launch_ks<2, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
     else if (p.nb == 2) launch_ks<2, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
     else launch_ks<2, 1, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
-  } else {
-    if (p.nb == 4) launch_ks<4, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
-    else launch_ks<4, 2, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
