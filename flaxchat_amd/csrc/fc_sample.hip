@@ -305,8 +305,10 @@ __device__ __forceinline__ void scan3(int v[3], int tot[3], int* sm) {
 // Round plan (one workgroup): packed chunks for draft step 0 (the row's
 // pending draft tokens), draft steps 1..k-1 (one token per active row) and
 // the verify pass (pending target tokens then the k drafts, which the draft
-// samplers write in place). Finished rows and rows waiting for a host
-// catch-up get no tokens.
+// samplers write in place). Finished rows get no tokens. A stalled row
+// (rollback backlog longer than FC_PMAX) drafts nothing: it re-feeds the next
+// FC_PMAX tokens of each model's backlog gen[len, gen_n - 1) at draft step 0
+// and in the verify chunk, until both caches hold everything before gen_n - 1.
 __global__ __launch_bounds__(PLAN_THR) void k_spec_plan(SpecDev s) {
   __shared__ int sm[48];
   const int P = FC_PMAX, K = s.k, B = s.B;
@@ -314,18 +316,33 @@ __global__ __launch_bounds__(PLAN_THR) void k_spec_plan(SpecDev s) {
   for (int b0 = 0; b0 < B; b0 += PLAN_THR) {
     const int b = b0 + threadIdx.x;
     const bool in = b < B;
-    const bool active = in && !s.stall[b] && !row_finished(s, b);
-    const int dn = active ? min(max(s.d_pend_n[b], 0), P) : 0;
-    const int tn = active ? min(max(s.t_pend_n[b], 0), P) : 0;
-    int v[3] = {dn, active ? 1 : 0, active ? tn + K : 0}, tot[3];
+    const bool live = in && !row_finished(s, b);
+    const bool refeed = live && s.stall[b];
+    const bool active = live && !refeed;
+    int dn = 0, tn = 0;
+    const int* gen = s.gen + (int64_t)(in ? b : 0) * s.gen_cap;
+    if (active) {
+      dn = min(max(s.d_pend_n[b], 0), P);
+      tn = min(max(s.t_pend_n[b], 0), P);
+    } else if (refeed) {
+      const int last = s.gen_n[b] - 1;
+      dn = min(max(last - s.d_len[b], 0), P);
+      tn = min(max(last - s.t_len[b], 0), P);
+    }
+    int v[3] = {dn, active ? 1 : 0, active ? tn + K : tn}, tot[3];
     scan3(v, tot, sm);
     if (in) {
       const int o0 = carry[0] + v[0], o1 = carry[1] + v[1], o2 = carry[2] + v[2];
       s.off_d0[b] = o0;
       s.off_ds[b] = o1;
       s.off_v[b] = o2;
-      for (int j = 0; j < dn; ++j) s.tok_d0[o0 + j] = s.d_pend[b * P + j];
-      for (int j = 0; j < tn; ++j) s.tok_v[o2 + j] = s.t_pend[b * P + j];
+      if (refeed) {
+        for (int j = 0; j < dn; ++j) s.tok_d0[o0 + j] = gen[s.d_len[b] + j];
+        for (int j = 0; j < tn; ++j) s.tok_v[o2 + j] = gen[s.t_len[b] + j];
+      } else {
+        for (int j = 0; j < dn; ++j) s.tok_d0[o0 + j] = s.d_pend[b * P + j];
+        for (int j = 0; j < tn; ++j) s.tok_v[o2 + j] = s.t_pend[b * P + j];
+      }
       const int dl = s.d_len[b];
       s.start_d[b] = dl;
       for (int i = 1; i < K; ++i) s.start_d[i * B + b] = dl + dn + i - 1;
@@ -413,26 +430,19 @@ __device__ void bookkeep(const SpecDev& s, int b, const int* emitted, int n_emit
     s.t_dirty[b] = BIG_POS;
     s.d_dirty[b] = BIG_POS;
     const int tp = gn - t_new, dp = gn - d_new;
-    if (tp <= P) {
-      s.t_len[b] = t_new;
+    s.t_len[b] = t_new;
+    s.d_len[b] = d_new;
+    if (tp <= P && dp <= P) {
       for (int i = 0; i < tp; ++i) s.t_pend[b * P + i] = gen[t_new + i];
       s.t_pend_n[b] = tp;
-    } else {  // host feeds gen[t_new, gn-1) then sets t_len = gn-1
-      s.t_len[b] = t_new;
-      s.t_pend[b * P] = gen[gn - 1];
-      s.t_pend_n[b] = 1;
-      flags |= 1;
-      s.stall[b] = 1;
-    }
-    if (dp <= P) {
-      s.d_len[b] = d_new;
       for (int i = 0; i < dp; ++i) s.d_pend[b * P + i] = gen[d_new + i];
       s.d_pend_n[b] = dp;
-    } else {
-      s.d_len[b] = d_new;
+    } else {  // the next rounds re-feed gen[len, gn-1) of both models (k_spec_plan)
+      s.t_pend[b * P] = gen[gn - 1];
+      s.t_pend_n[b] = 1;
       s.d_pend[b * P] = gen[gn - 1];
       s.d_pend_n[b] = 1;
-      flags |= 2;
+      flags |= 1;
       s.stall[b] = 1;
     }
   }
@@ -453,7 +463,7 @@ __device__ void bookkeep(const SpecDev& s, int b, const int* emitted, int n_emit
 // drafts, the greedy correction and greedy bonus go to `emitted`; a sampled
 // rejection or bonus is left as a draw request (mode / bonus_draw).
 struct Decision {
-  int mode;        // -1 finished, -2 stalled, 0 no rejection draw, 1 draw from p, 2 from the residual
+  int mode;        // -1 finished, -2 stalled (re-feeding), 0 no rejection draw, 1 draw from p, 2 from the residual
   int row;         // verify row of the rejection draw
   int n, acc, rej, bonus, kp;
   int bonus_draw;  // the bonus token is still to be drawn (sampling)
@@ -461,8 +471,8 @@ struct Decision {
 };
 static_assert(sizeof(Decision) == 32 * sizeof(int), "Decision layout");
 
-// mode -1: the row finished; -2: the row waits for a host catch-up and did
-// nothing this round.
+// mode -1: the row finished; -2: the row is stalled (it re-fed rollback
+// backlog this round and drafted nothing).
 __device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& d) {
   const int K = s.k, V = s.V;
   const bool greedy = !(s.T > 0.f);
@@ -523,11 +533,20 @@ __device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& 
   d.n = n;
 }
 
-// A finished row (flag 4) or a row waiting for its catch-up (flag 8): no
-// state change; the round counter of a waiting row does not move, so its
-// random stream does not depend on when the host catches it up.
+// A finished row (flag 4) or a stalled row that re-fed part of its backlog
+// this round (flag 8): the caches grew by the tokens k_spec_plan fed; once
+// both hold everything before gen_n - 1, the row resumes with that token
+// pending in each model (FC_PMAX-sized pending lists are exact from then on).
+// The round counter of a stalled row does not move, so its random stream
+// does not depend on how many rounds the re-feed takes.
 __device__ void idle_row(const SpecDev& s, int b, int mode) {
   int* res = s.result + (int64_t)b * FC_RES_STRIDE;
+  if (mode == -2) {
+    const int last = s.gen_n[b] - 1;
+    s.d_len[b] += s.off_d0[b + 1] - s.off_d0[b];
+    s.t_len[b] += s.off_v[b + 1] - s.off_v[b];  // a stalled row has no drafts in the verify chunk
+    if (s.d_len[b] >= last && s.t_len[b] >= last) s.stall[b] = 0;
+  }
   res[0] = 0; res[1] = 0; res[2] = -1; res[3] = mode == -2 ? 8 : 4; res[4] = 0;
   res[5] = s.t_pend_n[b]; res[6] = s.d_pend_n[b];
   if (mode != -2) s.round[b] += 1;

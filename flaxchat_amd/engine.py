@@ -96,8 +96,9 @@ class SpecSession:
     graph that every later round replays. The host keeps `depth` rounds in
     flight: each round's result record is copied to its own pinned slot, and
     round r is read while round r + 1 runs. A row whose rollback needs more
-    than FC_PMAX re-fed tokens stalls on the device (it is fed nothing and its
-    round counter does not move) until the host has fed the missing tokens.
+    than FC_PMAX re-fed tokens stalls on the device: it drafts nothing and
+    re-feeds FC_PMAX tokens of its backlog per round (its round counter does
+    not move) until both caches have caught up; the host is not involved.
     """
 
     def __init__(self, target: DeviceModel, draft: DeviceModel, rows: List[List[int]], max_tokens: int,
@@ -151,7 +152,7 @@ class SpecSession:
                                  *[self.bufs[n].data_ptr() for n in _lib._SPEC_PTRS],
                                  self.bufs["part"].data_ptr(), self.bufs["part"].numel())
         self.ws = Workspace(dev)          # captured by the round graph: never reallocated after capture
-        self.ws_catchup = Workspace(dev)  # prefill / catch-up
+        self.ws_prefill = Workspace(dev)
         nb = lib().fc_spec_workspace_bytes(ctypes.byref(target.desc), ctypes.byref(draft.desc), B, k)
         if nb < 0:
             raise RuntimeError("fc_spec_workspace_bytes failed")
@@ -162,13 +163,15 @@ class SpecSession:
         self.res_h = [torch.empty(B, RES_STRIDE, dtype=torch.int32, pin_memory=True) for _ in range(self.depth)]
         self.rounds = 0
         self.accept_hist = []
+        self.stalls = 0         # rollbacks longer than FC_PMAX (row stalled to re-feed)
+        self.refeed_rounds = 0  # row-rounds spent re-feeding such a backlog
 
     # ------------------------------------------------------------ phases
     def prefill(self):
         b = self.bufs
         with torch.cuda.stream(self.stream):
             for dm, cache in ((self.T, self.tcache), (self.Dm, self.dcache)):
-                prefill_rows(dm, cache, [r[:-1] for r in self.rows], [0] * self.B, self.ws_catchup)
+                prefill_rows(dm, cache, [r[:-1] for r in self.rows], [0] * self.B, self.ws_prefill)
             P = np.array([len(r) for r in self.rows], np.int32)
             last = np.array([r[-1] for r in self.rows], np.int32)
             gen = np.zeros((self.B, self.gen_cap), np.int32)
@@ -213,41 +216,13 @@ class SpecSession:
             self._round_call()
         self.launched += 1
 
-    def _catch_up(self, flags):
-        """Rows whose rollback point lies more than FC_PMAX tokens back (after
-        a last-index rejection marked the caches stale): feed the missing
-        tokens so each model has exactly one pending token, then release the
-        row. The caller has drained the stream."""
-        b = self.bufs
-        gen = b["gen"].cpu().numpy()
-        gen_n = b["gen_n"].cpu().numpy()
-        for bit, dm, cache, key in ((1, self.T, self.tcache, "t_len"), (2, self.Dm, self.dcache, "d_len")):
-            sel = (flags & bit) != 0
-            if not sel.any():
-                continue
-            lens = b[key].cpu().numpy()
-            rows, starts = [], []
-            for i in range(self.B):
-                if sel[i]:
-                    rows.append(gen[i, lens[i]:gen_n[i] - 1].tolist())
-                    starts.append(int(lens[i]))
-                else:
-                    rows.append([])
-                    starts.append(0)
-            with torch.cuda.stream(self.stream):
-                prefill_rows(dm, cache, rows, starts, self.ws_catchup)
-                new = np.where(sel, gen_n - 1, lens).astype(np.int32)
-                b[key].copy_(torch.from_numpy(new))
-        with torch.cuda.stream(self.stream):
-            st = b["stall"].cpu().numpy()
-            st[(flags & 3) != 0] = 0
-            b["stall"].copy_(torch.from_numpy(st))
-
     def _record(self, res) -> int:
         active = res[:, 4] > 0
         if active.any():
             self.rounds += 1
             self.accept_hist.append(res[active, 1].copy())
+        self.stalls += int(((res[:, 3] & 1) != 0).sum())
+        self.refeed_rounds += int(((res[:, 3] & 8) != 0).sum())
         return int(np.bitwise_or.reduce(res[:, 3]))
 
     def run(self, max_rounds: Optional[int] = None):
@@ -273,19 +248,7 @@ class SpecSession:
             ev.synchronize()
             res = self.res_h[slot].numpy().copy()
             self._record(res)
-            flags = res[:, 3]
-            if (flags & 3).any():
-                flags = flags.copy()
-                while inflight:  # later rounds left the stalled rows alone; other rows may stall too
-                    ev2, slot2 = inflight.popleft()
-                    ev2.synchronize()
-                    res2 = self.res_h[slot2].numpy().copy()
-                    self._record(res2)
-                    flags |= res2[:, 3] & 3
-                self.stream.synchronize()
-                self._catch_up(flags)
-                continue
-            if ((flags & 4) != 0).all():
+            if ((res[:, 3] & 4) != 0).all():
                 stop = True
 
     def outputs(self) -> List[List[int]]:

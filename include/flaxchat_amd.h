@@ -129,8 +129,8 @@ typedef struct fc_spec_state {
   int32_t* gen;    int32_t* gen_n;       /* [B][gen_cap] tokens incl. prompt   */
   int32_t* prompt_len;                   /* [B]                                */
   int32_t* round;                        /* [B] round counter (Philox)         */
-  int32_t* stall;                        /* [B] nonzero: row waits for the host */
-                                         /* catch-up (more than FC_PMAX pending) */
+  int32_t* stall;                        /* [B] nonzero: row re-feeds a rollback */
+                                         /* backlog longer than FC_PMAX           */
   int32_t* result;                       /* [B][FC_RES_STRIDE]                 */
   /* per-round scratch (chunks in the packed layout) */
   int32_t* tok_d0;   /* [B*FC_PMAX]     draft step 0 tokens                    */
@@ -154,13 +154,15 @@ typedef struct fc_spec_state {
 #define FC_PMAX 16
 /* Tokens a model still has to be fed (fed next round ahead of the drafts):
  * normally 1 (target) or 1-2 (draft); after a rejection that rolls back past
- * a stale cache entry, up to FC_PMAX. Result row layout: [0] n_emitted this
- * round, [1] accepted, [2] rejected index or -1, [3] flags (bit0 target
- * needs catch-up, bit1 draft needs catch-up: more than FC_PMAX pending, the
- * row then stalls until the host feeds the missing tokens and clears
- * stall[b]; bit2 row finished; bit3 row stalled this round, nothing done),
- * [4] k', [5] target pending count, [6] draft pending count,
- * [8..8+k+1] emitted tokens. */
+ * a stale cache entry, up to FC_PMAX. A longer rollback stalls the row: the
+ * following rounds re-feed FC_PMAX tokens of each model's backlog
+ * gen[len, gen_n - 1) per round, without drafting, until both caches hold
+ * everything before gen_n - 1 (stall[b] then returns to 0). Result row
+ * layout: [0] n_emitted this round, [1] accepted, [2] rejected index or -1,
+ * [3] flags (bit0 the rollback stalled the row; bit2 row finished; bit3 the
+ * row was stalled this round: backlog re-fed, nothing emitted), [4] k',
+ * [5] target pending count, [6] draft pending count, [8..8+k+1] emitted
+ * tokens. */
 
 const char* fc_last_error(void);
 int32_t fc_version(void);

@@ -119,6 +119,66 @@ def test_spec_greedy_quirk_coverage(tiny_pair):
     assert got == refs
 
 
+def _long_rollbacks(rec, plen, pmax=16):
+    """Backlogs the engine must re-feed over several rounds: after a
+    last-index rejection leaves a stale entry (flaxchat/engine.py:573), a
+    later rejection re-prefills (engine.py:593-606) from that entry; the
+    engine re-feeds gen[stale, end) and stalls the row when that is longer
+    than FC_PMAX."""
+    gn, stale, out = plen, None, []
+    for r in rec:
+        kp = len(r["drafts"])
+        g0 = gn
+        gn += len(r["emitted"])
+        if r["accepted"] == kp:
+            if r["rej"] >= 0:
+                stale = g0 + kp - 1 if stale is None else min(stale, g0 + kp - 1)
+        else:
+            if stale is not None and gn - stale > pmax:
+                out.append(gn - stale)
+            stale = None
+    return out
+
+
+@pytest.mark.parametrize("T,k", [(0.0, 3), (0.8, 4)])
+def test_spec_long_rollback_refeed(T, k):
+    """A draft close to the target (a copy with resid_lambdas + 0.1) accepts
+    long runs, so some rows roll back more than FC_PMAX tokens; those rows
+    stall and re-feed the backlog on the device over several rounds. The
+    streams must still equal the oracle's."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    from oracle.spec import spec_literal
+    cfg = GPTConfig(sequence_len=256, vocab_size=256, n_layer=2, n_head=2, n_kv_head=2, n_embd=64,
+                    window_pattern="SL", short_window=8)
+    tgt = GPT.init_normal(cfg, seed=0, std=0.1).perturb_scalars()
+    draft = tgt.make_draft(2)
+    draft.resid_lambdas = (draft.resid_lambdas + 0.1).astype(np.float32)
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 256, 5).tolist() for _ in range(6)]
+    refs, long_rb = [], []
+    for b, p in enumerate(prompts):
+        rec = []
+        refs.append(spec_literal(tgt, draft, p, max_tokens=120, temperature=T, top_k=40, seed=3, draft_steps=k,
+                                 row=b, record=rec))
+        long_rb += _long_rollbacks(rec, len(p))
+    assert long_rb, "test configuration no longer produces a rollback longer than FC_PMAX"
+    _say(f"spec long rollback T={T} k={k}: backlogs {long_rb}")
+    target = as_device_model(tgt, "fp32")
+    dm = as_device_model(draft, "fp32")
+    s = SpecSession(target, dm, prompts, 120, T, 40, 3, k)
+    try:
+        s.prefill()
+        s.run()
+        got = s.outputs()
+    finally:
+        s.close()
+    assert s.stalls == len(long_rb)
+    assert s.refeed_rounds >= s.stalls
+    for b in range(len(prompts)):
+        assert got[b] == refs[b], f"row {b}"
+
+
 def test_spec_cfg1_greedy(cfg1_pair):
     """batch 1, prompt 32, 64 new tokens, greedy, k=4."""
     from oracle.spec import spec_literal
