@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ x, TO* __re
 }
 
 struct FwdWork {
-  float *x, *x0, *xb, *qkv;
+  float *x, *x0, *xb, *qkv, *ssq;
   void *h, *q, *y, *hid, *part;
   int *tok_row, *tok_pos;
   int64_t part_bytes, total;
@@ -246,6 +246,7 @@ static FwdWork carve(const fc_model* m, int B, int max_tokens, int max_per_row, 
   w.q = take(M * H * hd * es);
   w.y = take(M16 * H * hd * es);
   w.hid = take(M16 * 4 * D * es);
+  w.ssq = (float*)take((int64_t)(D / 16) * M * 4);  // folded norm: per 16+ column tile and row
   w.tok_row = (int*)take(M * 4);
   w.tok_pos = (int*)take(M * 4);
   // attention splits are sized for the largest key range a cache can hold
@@ -307,6 +308,10 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   const int es = dt == FC_BF16 ? 2 : 4;
   const int typ_per_row = std::max(1, (Mtyp + B - 1) / B);
   const bool fuse_qkv = fc_gemm_fuses_qkv(Mtyp, NQKV, D, dt, hd);
+  // bf16: the RMSNorm between attention and MLP is folded into the GEMMs (the
+  // attention c_proj keeps a bf16 copy of x and per-tile sums of squares,
+  // c_fc scales its rows by 1 / rms); fp32 keeps the exact RMSNorm kernel
+  const bool fold = dt == FC_BF16 && fc_gemm_fold_ok(Mtyp, D);
 
   if (dt == FC_BF16)
     hipLaunchKernelGGL(k_embed<bf16_t>, dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
@@ -377,21 +382,34 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.out = w.x;
     e.ldo = D;
     int S = 1;
-    rc = fc_launch_gemm(w.y, L.wo, Mcap, Mdev, Mtyp, D, H * hd, dt, e, w.gw, s, &S);
-    if (rc) return rc;
-    if (S > 1) {
-      pend.S = S;
-      pend.mode = EPI_ADD;
-      pend.rows = Mcap;
-      pend.part = w.gw.part;
+    if (fold) {  // x += attn; h = bf16(x) and per-tile sums of squares for c_fc
+      e.xa = (uint16_t*)w.h;
+      e.ssq = w.ssq;
+      e.ssq_ld = Mcap;
+      rc = fc_launch_gemm(w.y, L.wo, Mcap, Mdev, Mtyp, D, H * hd, dt, e, w.gw, s, nullptr);
+      if (rc) return rc;
+    } else {
+      rc = fc_launch_gemm(w.y, L.wo, Mcap, Mdev, Mtyp, D, H * hd, dt, e, w.gw, s, &S);
+      if (rc) return rc;
+      if (S > 1) {
+        pend.S = S;
+        pend.mode = EPI_ADD;
+        pend.rows = Mcap;
+        pend.part = w.gw.part;
+      }
+      norm(Mcap, 0);
+      FC_LAUNCH_CHECK();
     }
-    norm(Mcap, 0);
-    FC_LAUNCH_CHECK();
     e = Epi{};
     e.mode = EPI_RELU2;
     e.out = w.hid;
     e.ldo = 4 * D;
     e.out_dtype = dt;
+    if (fold) {
+      e.rms_in = w.ssq;
+      e.rms_n = fc_gemm_fold_tiles(Mtyp, D);
+      e.ssq_ld = Mcap;
+    }
     rc = fc_launch_gemm(w.h, L.wfc, Mcap, Mdev, Mtyp, 4 * D, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
     e = Epi{};

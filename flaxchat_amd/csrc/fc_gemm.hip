@@ -63,6 +63,35 @@ __device__ __forceinline__ void epi_apply(const Epi e, int m, int n, float acc) 
   }
 }
 
+// Folded RMSNorm, consumer side: the 256 / MT threads of each output row
+// (consecutive lanes) each load up to FC_RMS_REG of the row's per-tile sums
+// of squares at kernel start (clamped, unconditional: one batch of loads in
+// flight together) and keep them in registers through the K loop, whose
+// loads they precede; the epilogue adds them up over those lanes (a fixed
+// shuffle tree: deterministic).
+#define FC_RMS_REG 16
+struct RmsPre {
+  float v[FC_RMS_REG];
+};
+template <int MT>
+__device__ __forceinline__ void rms_load(RmsPre& r, const Epi& e, int m0, int M) {
+  constexpr int TPR = 256 / MT;
+  const int m = min(m0 + (int)threadIdx.x / TPR, M - 1), sub = (int)threadIdx.x % TPR;
+#pragma unroll
+  for (int j = 0; j < FC_RMS_REG; ++j) r.v[j] = e.rms_in[(int64_t)min(sub + j * TPR, e.rms_n - 1) * e.ssq_ld + m];
+}
+template <int MT>
+__device__ __forceinline__ float rms_finish(const RmsPre& r, const Epi& e, int K) {
+  constexpr int TPR = 256 / MT;
+  const int sub = (int)threadIdx.x % TPR;
+  float p = 0.f;
+#pragma unroll
+  for (int j = 0; j < FC_RMS_REG; ++j) p += sub + j * TPR < e.rms_n ? r.v[j] : 0.f;
+#pragma unroll
+  for (int o = TPR / 2; o > 0; o >>= 1) p += __shfl_xor(p, o, WAVE);
+  return 1.f / sqrtf(p / (float)K + 1e-6f);
+}
+
 // ---------------------------------------------------------------------------
 // VALU GEMV / small GEMM. 256 threads = 4 waves; each wave owns 4 columns
 // and MB rows; lanes split K in 16-byte vectors.
@@ -205,6 +234,10 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
   const int C = K >> 6;
   const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
   const int nch = c_end - c_beg > wave ? (c_end - c_beg - wave + 3) >> 2 : 0;
+  RmsPre rpre;  // folded RMSNorm: this thread's share of its output row's sums of squares
+  if constexpr (EPI == EPI_RELU2) {
+    if (e.rms_in != nullptr) rms_load<MT>(rpre, e, m0, M);
+  }
 
   f32x4 acc[MB][NB];
 #pragma unroll
@@ -295,14 +328,49 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
   const int t = threadIdx.x;
   const int row = t / TPR, col0 = (t - row * TPR) * OPT;
   const int m = m0 + row;
-  if (m >= M) return;
+  const bool live = m < M;
+  float v[OPT];
+#pragma unroll
+  for (int c = 0; c < OPT; ++c)
+    v[c] = red[0][row][col0 + c] + red[1][row][col0 + c] + red[2][row][col0 + c] + red[3][row][col0 + c];
+  if constexpr (EPI == EPI_RELU2) {
+    if (e.rms_in != nullptr) {  // thread t's epilogue row is its prefetch row (t / TPR)
+      static_assert(TPR == 256 / MT, "row mapping");
+      const float sc = rms_finish<MT>(rpre, e, K);
+#pragma unroll
+      for (int c = 0; c < OPT; ++c) v[c] *= sc;
+    }
+  }
+  if constexpr (EPI == EPI_ADD) {
+    if (e.xa != nullptr) {
+      // residual add, bf16 copy of the new x (OPT consecutive columns: whole
+      // bf16 pairs in fragment order) and the row's sum of squares over this
+      // tile (the TPR threads of a row are consecutive lanes)
+      static_assert(OPT % 2 == 0 && 64 % TPR == 0, "folded-norm epilogue tiling");
+      float ss = 0.f;
+      if (live) {
+        float* o = (float*)e.out + (int64_t)m * e.ldo + n0 + col0;
+#pragma unroll
+        for (int c = 0; c < OPT; c += 2) {
+          const float a0 = o[c] + v[c], a1 = o[c + 1] + v[c + 1];
+          o[c] = a0;
+          o[c + 1] = a1;
+          ss += a0 * a0 + a1 * a1;
+          *(uint32_t*)(e.xa + frag_idx(m, n0 + col0 + c, (int)e.ldo)) =
+              (uint32_t)f2bf(a0) | ((uint32_t)f2bf(a1) << 16);
+        }
+      }
+#pragma unroll
+      for (int o = TPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, WAVE);
+      if (live && col0 == 0) e.ssq[(int64_t)nt * e.ssq_ld + m] = ss;
+      return;
+    }
+  }
+  if (!live) return;
   Epi ee = e;
   ee.split = s;
 #pragma unroll
-  for (int c = 0; c < OPT; ++c) {
-    const float v = red[0][row][col0 + c] + red[1][row][col0 + c] + red[2][row][col0 + c] + red[3][row][col0 + c];
-    epi_apply<EPI>(ee, m, n0 + col0 + c, v);
-  }
+  for (int c = 0; c < OPT; ++c) epi_apply<EPI>(ee, m, n0 + col0 + c, v[c]);
 }
 
 // Attention prologue of one token and one head slot from its fp32 GEMM
@@ -442,6 +510,10 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #pragma unroll
   for (int j = 0; j < NBW; ++j) wbase[j] = W + (int64_t)(n0 / 16 + wave * NBW + j) * KS32 * 512 + lane * 8;
 
+  RmsPre rpre;  // folded RMSNorm: this thread's share of row m0 + t / (256 / MT)
+  if constexpr (EPI == EPI_RELU2) {
+    if (e.rms_in != nullptr) rms_load<16 * MB>(rpre, e, m0, M);
+  }
   f32x4 acc[MB][NBW];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -512,6 +584,26 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
     __syncthreads();
     qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7);
   } else {
+    // folded RMSNorm (RELU2 reading the bf16 copy of x): acc row
+    // 16 mb + 4 g + i takes the factor lane 4 g + i computed for its row
+    float rsc[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rsc[mb][i] = 1.f;
+    if constexpr (EPI == EPI_RELU2) {
+      if (e.rms_in != nullptr) {
+        constexpr int MT = 16 * MB;
+        __shared__ float rowinv[MT];
+        const float inv = rms_finish<MT>(rpre, e, K);
+        if (threadIdx.x % (256 / MT) == 0) rowinv[threadIdx.x / (256 / MT)] = inv;
+        __syncthreads();
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rsc[mb][i] = rowinv[16 * mb + 4 * g + i];
+      }
+    }
     Epi ee = e;
     ee.split = s;
 #pragma unroll
@@ -521,7 +613,7 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = m0 + 16 * mb + 4 * g + i;
-          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i]);
+          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i] * rsc[mb][i]);
         }
   }
 }
@@ -651,6 +743,25 @@ bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
   return p.la && p.mb == 2 && p.nb == 2;
 }
 
+// The EPI_ADD GEMM that writes the bf16 copy of x (attention c_proj, bf16):
+// unsplit K-split kernel, 32 x 16 tiles for draft rows, 32 x 64 for verify rows.
+static GemmPlan plan_fold_add(int Mtyp, int N) {
+  GemmPlan p{};
+  p.S = 1;
+  p.mb = Mtyp <= 16 ? 1 : 2;
+  p.nb = Mtyp <= 16 ? 2 : (Mtyp <= 32 ? 1 : 4);
+  while (p.nb > 1 && N % (16 * p.nb) != 0) p.nb /= 2;
+  if (p.nb == 1 && p.mb != 2) p.nb = 2;
+  return p;
+}
+int fc_gemm_fold_tiles(int Mtyp, int N) { return N / (16 * plan_fold_add(Mtyp, N).nb); }
+// the consumer (c_fc: N = 4 D, K = D) prefetches FC_RMS_REG tiles per thread
+// with 256 / MT threads per row
+bool fc_gemm_fold_ok(int Mtyp, int D) {
+  const GemmPlan c = plan_gemm(Mtyp, 4 * D, D, FC_BF16, false);
+  return !c.gemv && fc_gemm_fold_tiles(Mtyp, D) <= FC_RMS_REG * (256 / (16 * c.mb));
+}
+
 int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K) {
   if (Mtyp <= 0 || Mcap <= 0 || N <= 0 || K <= 0) return 0;
   GemmPlan p = plan_gemm(Mtyp, N, K, FC_BF16, true);
@@ -673,6 +784,10 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   }
   const bool can_split = splits != nullptr && gw.part != nullptr;
   GemmPlan p = plan_gemm(Mtyp, N, K, dtype, can_split);
+  if (e.mode == EPI_ADD && e.xa != nullptr) {
+    FC_CHECK_ARG(dtype == FC_BF16 && e.ssq != nullptr && !can_split, "folded-norm GEMM: bf16, ssq, no split");
+    p = plan_fold_add(Mtyp, N);
+  }
   if (p.S > 1 && (int64_t)p.S * Mcap * N * 4 > gw.part_bytes) p.S = 1;
   Epi ee = e;
   if (p.S > 1) {

@@ -38,6 +38,17 @@ struct Epi {
   float* part;
   int part_rows, split;
   QkvEpi qkv;
+  // The attention-side RMSNorm folded into the GEMMs (bf16; flaxchat/gpt.py:44-46,
+  // engine.py:160-161): EPI_ADD given `xa` (unsplit, K-split kernel) also
+  // writes bf16(new x) in fragment order to xa, the c_fc operand, and for
+  // row m and its column tile nt the sum of squares of the new x over the
+  // tile to ssq[nt * ssq_ld + m]; a GEMM given `rms_in` multiplies output row
+  // m by 1 / sqrt(sum_{t < rms_n} rms_in[t * ssq_ld + m] / K + 1e-6) (summed in
+  // a fixed order).
+  uint16_t* xa;
+  float* ssq;
+  const float* rms_in;
+  int ssq_ld, rms_n;
 };
 
 #define FC_MAX_SPLIT 8
@@ -47,6 +58,10 @@ struct GemmWork {
   int64_t part_bytes;
 };
 int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K);
+// column tiles of the EPI_ADD GEMM that writes `xa` (the rms_n of its consumer),
+// and whether its consumers can take that many
+int fc_gemm_fold_tiles(int Mtyp, int N);
+bool fc_gemm_fold_ok(int Mtyp, int D);
 // `splits` (may be NULL: no split) receives the split count; when > 1 the
 // output was written as partials to gw.part and the caller must finish it.
 // true when the GEMM of this shape runs the tile that can finish the
