@@ -77,6 +77,33 @@ def test_forward_logits_vs_oracle(which, dtype, tiny_pair, cfg1_pair):
     assert err < (1e-3 if dtype == "fp32" else 5e-2)
 
 
+def test_single_token_rows_bf16(cfg1_pair):
+    """Rows of different lengths fed one token each per step (the draft-step
+    chunk shape), in bf16, against the oracle."""
+    tgt = cfg1_pair[0]
+    dm = as_device_model(tgt, "bf16")
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, 8192, n).tolist() for n in (5, 9, 2)]
+    steps = 6
+    nxt = [rng.integers(0, 8192, steps).tolist() for _ in prompts]
+    B = len(prompts)
+    cache = DeviceCache(dm, B, 64)
+    ws = Workspace(dm.device)
+    forward_rows(dm, cache, prompts, [0] * B, 0, None, ws)
+    got = []
+    for i in range(steps):
+        lg = torch.zeros(B, 1, dm.V, device=dm.device)
+        forward_rows(dm, cache, [[nxt[b][i]] for b in range(B)], [len(prompts[b]) + i for b in range(B)], 1, lg, ws)
+        got.append(lg[:, 0].cpu().numpy())
+    torch.cuda.synchronize()
+    err = 0.0
+    for b in range(B):
+        ref = _oracle_logits(tgt, prompts[b] + nxt[b])[len(prompts[b]):]
+        err = max(err, np.abs(np.stack([g[b] for g in got]) - ref).max())
+    _say(f"single-token rows bf16: max abs err {err:.3e}")
+    assert err < 5e-2
+
+
 def test_chunk_equals_steps(cfg1_pair):
     tgt = cfg1_pair[0]
     toks = np.random.default_rng(6).integers(0, 8192, 24).tolist()
