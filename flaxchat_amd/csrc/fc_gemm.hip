@@ -453,6 +453,62 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
   }
 }
 
+// Epilogue of the column-split kernels (k_gemm_la, k_gemm_dma): acc[mb][j]
+// holds rows 16 mb + 4 g + i, column 16 (wave NBW + j) + r of the tile.
+template <int MB, int NBW, int EPI>
+__device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[MB][NBW], const RmsPre& rpre, int m0,
+                                              int n0, int nt, int s, int M, int K) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  if constexpr (EPI == EPI_QKV) {
+    // the tile is one head (column tile nt = head slot) for 32 tokens: stage
+    // it in LDS, then 8 threads per token finish it (16 dims each: d and
+    // d + 64 of 8 rotary pairs)
+    static_assert(MB == 2 && NBW == 2, "EPI_QKV needs 32 x 128 tiles");
+    __shared__ float T[32][128 + 4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) T[16 * mb + 4 * g + i][16 * (wave * NBW + j) + r] = acc[mb][j][i];
+    __syncthreads();
+    qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7);
+  } else {
+    // folded RMSNorm (RELU2 reading the bf16 copy of x): acc row
+    // 16 mb + 4 g + i takes the factor lane 4 g + i computed for its row
+    float rsc[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rsc[mb][i] = 1.f;
+    if constexpr (EPI == EPI_RELU2) {
+      if (e.rms_in != nullptr) {
+        constexpr int MT = 16 * MB;
+        __shared__ float rowinv[MT];
+        const float inv = rms_finish<MT>(rpre, e, K);
+        if (threadIdx.x % (256 / MT) == 0) rowinv[threadIdx.x / (256 / MT)] = inv;
+        __syncthreads();
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rsc[mb][i] = rowinv[16 * mb + 4 * g + i];
+      }
+    }
+    Epi ee = e;
+    ee.split = s;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + 16 * mb + 4 * g + i;
+          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i] * rsc[mb][i]);
+        }
+  }
+}
+
 // bf16 MFMA GEMM for larger row counts, A shared through LDS.
 //
 // A workgroup owns an MT x NT tile (MT = 16 MB rows, NT = 64 NBW columns);
@@ -569,53 +625,123 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #undef LA_STAGE_A
   }
 
-  if constexpr (EPI == EPI_QKV) {
-    // the tile is one head (column tile nt = head slot) for 32 tokens: stage
-    // it in LDS, then 8 threads per token finish it (16 dims each: d and
-    // d + 64 of 8 rotary pairs)
-    static_assert(MB == 2 && NBW == 2, "EPI_QKV needs 32 x 128 tiles");
-    __shared__ float T[32][128 + 4];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < NBW; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) T[16 * mb + 4 * g + i][16 * (wave * NBW + j) + r] = acc[mb][j][i];
-    __syncthreads();
-    qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7);
+  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, m0, n0, nt, s, M, K);
+}
+
+// bf16 MFMA GEMM for verify-size row counts with both operands staged in an
+// LDS ring by direct global-to-LDS loads.
+//
+// Same tile and column split as k_gemm_la (MT = 16 MB rows, NT = 64 NBW
+// columns, each wave owns 16 NBW columns), but the activation blocks and the
+// wave's own weight blocks of a 64-wide k chunk go straight from global
+// memory into one of four LDS stages (no registers held by loads in flight):
+// while chunk i computes, chunks i+1 and i+2 are loading. Each stage is its
+// own LDS object and the loop is unrolled over the four, so the compiler can
+// tell a stage's reads from the loads into the others and waits only for the
+// chunk it needs (vmcnt(two chunks' loads)), then a plain barrier makes every
+// wave's part of the stage visible. The stage refilled at step i is the one
+// read at step i-1, which every wave has finished by the barrier of step i.
+// Grid and tile order as in k_gemm_la.
+template <int MB, int NBW>
+struct DmaStage {
+  uint4 a[2 * MB][64];
+  uint4 w[4][2 * NBW][64];
+};
+template <int MB, int NBW, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                  int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
+                                                  int mtiles, int mfast, Epi e) {
+  constexpr int WAVES = 4, AB = 2 * MB, NSTG = 4;
+  static_assert(AB % WAVES == 0, "the A blocks of a chunk split evenly over the waves");
+  __shared__ DmaStage<MB, NBW> s0, s1, s2, s3;
+  const int id = blockIdx.x;
+  const int ntiles8 = (ntiles + 7) & ~7;
+  int nt, mt;
+  if (mfast) {
+    const int xcd = id & 7, loc = id >> 3;
+    const int nl = loc / mtiles;
+    mt = loc - nl * mtiles;
+    nt = nl * 8 + xcd;
   } else {
-    // folded RMSNorm (RELU2 reading the bf16 copy of x): acc row
-    // 16 mb + 4 g + i takes the factor lane 4 g + i computed for its row
-    float rsc[MB][4];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rsc[mb][i] = 1.f;
-    if constexpr (EPI == EPI_RELU2) {
-      if (e.rms_in != nullptr) {
-        constexpr int MT = 16 * MB;
-        __shared__ float rowinv[MT];
-        const float inv = rms_finish<MT>(rpre, e, K);
-        if (threadIdx.x % (256 / MT) == 0) rowinv[threadIdx.x / (256 / MT)] = inv;
-        __syncthreads();
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) rsc[mb][i] = rowinv[16 * mb + 4 * g + i];
-      }
-    }
-    Epi ee = e;
-    ee.split = s;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int j = 0; j < NBW; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = m0 + 16 * mb + 4 * g + i;
-          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i] * rsc[mb][i]);
-        }
+    nt = id % ntiles8;
+    mt = id / ntiles8;
   }
+  if (nt >= ntiles) return;
+  const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
+  const int m0 = mt * 16 * MB;
+  if (m0 >= M) return;
+  const int n0 = nt * 64 * NBW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t KS32 = K >> 5;
+  const int C = K >> 6;
+  const int last_blk = (M - 1) >> 4;
+  const bf16_t* wbase = W + ((int64_t)(n0 / 16 + wave * NBW)) * KS32 * 512 + lane * 8;
+  const bf16_t* abase[AB / WAVES];
+#pragma unroll
+  for (int u = 0; u < AB / WAVES; ++u) {
+    const int q = wave + WAVES * u;  // row block q / 2, k step q % 2
+    abase[u] = A + ((int64_t)min(m0 / 16 + (q >> 1), last_blk) * KS32 + (q & 1)) * 512 + lane * 8;
+  }
+  RmsPre rpre;  // folded RMSNorm: this thread's share of row m0 + t / (256 / MT)
+  if constexpr (EPI == EPI_RELU2 || EPI == EPI_QKV) {
+    if (e.rms_in != nullptr) rms_load<16 * MB>(rpre, e, m0, M);
+  }
+  f32x4 acc[MB][NBW];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // loads per chunk and wave: 2 NBW weight blocks + AB / WAVES activation blocks
+  constexpr int PER = 2 * NBW + AB / WAVES;
+  constexpr int NV = PER * (NSTG - 2);
+  static_assert(NV < 64, "vmcnt range");
+#define DMA_ISSUE(S, c_)                                                                             \
+  {                                                                                                  \
+    const int c = min((c_), C - 1); /* past the end: harmless re-reads into an unread stage */       \
+    _Pragma("unroll") for (int j = 0; j < NBW; ++j)                                                  \
+      _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                                               \
+        __builtin_amdgcn_global_load_lds((const void*)(wbase + ((int64_t)j * KS32 + 2 * c + ks) * 512), \
+                                         (__attribute__((address_space(3))) void*)&S.w[wave][2 * j + ks][0], 16, 0, 0); \
+    _Pragma("unroll") for (int u = 0; u < AB / WAVES; ++u)                                           \
+      __builtin_amdgcn_global_load_lds((const void*)(abase[u] + (int64_t)c * 1024),                  \
+                                       (__attribute__((address_space(3))) void*)&S.a[wave + WAVES * u][0], 16, 0, 0); \
+  }
+#define DMA_STEP(S, SN, i_)                                                                          \
+  {                                                                                                  \
+    __builtin_amdgcn_s_waitcnt((NV & 15) | ((NV >> 4) << 14) | (7 << 4) | (15 << 8));                \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    __builtin_amdgcn_s_barrier();                                                                    \
+    __builtin_amdgcn_sched_barrier(0);                                                               \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                         \
+    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                               \
+      v4u w[NBW];                                                                                    \
+      _Pragma("unroll") for (int j = 0; j < NBW; ++j) w[j] = __builtin_bit_cast(v4u, S.w[wave][2 * j + ks][lane]); \
+      _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                            \
+        const v4u a = __builtin_bit_cast(v4u, S.a[2 * mb + ks][lane]);                               \
+        _Pragma("unroll") for (int j = 0; j < NBW; ++j) acc[mb][j] = mfma16(a, w[j], acc[mb][j]);    \
+      }                                                                                              \
+    }                                                                                                \
+    DMA_ISSUE(SN, (i_) + NSTG - 1);                                                                  \
+  }
+  DMA_ISSUE(s0, 0);
+  DMA_ISSUE(s1, 1);
+  DMA_ISSUE(s2, 2);
+  int i = 0;
+  for (; i + 3 < C; i += 4) {
+    DMA_STEP(s0, s3, i);
+    DMA_STEP(s1, s0, i + 1);
+    DMA_STEP(s2, s1, i + 2);
+    DMA_STEP(s3, s2, i + 3);
+  }
+  if (i < C) DMA_STEP(s0, s3, i);
+  if (i + 1 < C) DMA_STEP(s1, s0, i + 1);
+  if (i + 2 < C) DMA_STEP(s2, s1, i + 2);
+#undef DMA_STEP
+#undef DMA_ISSUE
+  __builtin_amdgcn_s_waitcnt(0);  // no direct load outlives the workgroup's LDS
+  __syncthreads();                // the epilogue may reuse LDS
+  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, m0, n0, nt, 0, M, K);
 }
 
 // ---------------------------------------------------------------------------
@@ -672,6 +798,16 @@ static void launch_la(const void* A, const void* W, int Mcap, const int* Mdev, i
                                            mfast, e));
 }
 
+template <int MB, int NBW>
+static void launch_dma(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
+                       hipStream_t s) {
+  const int ntiles = N / (64 * NBW), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
+  const int nwg = (ntiles + 7) / 8 * 8 * mtiles;
+  const int mfast = Mdev == nullptr ? 1 : 0;
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_dma<MB, NBW, E>), dim3(nwg), dim3(256), 0, s, (const bf16_t*)A,
+                                           (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, mtiles, mfast, e));
+}
+
 static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
                           hipStream_t s) {
   const int ntiles = N / 128, mtiles = (Mcap + 31) / 32;
@@ -684,9 +820,12 @@ static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mde
 // the K split are chosen for the typical row count Mtyp (the grid covers
 // Mcap rows; tiles past the device-side count exit at once).
 struct GemmPlan {
-  bool gemv, la;  // VALU GEMV (fp32) / LDS-shared-A kernel (else the K-split kernel)
-  int mb, nb, S;  // k_gemm_ks: 16 mb x 16 nb tile; k_gemm_la: 16 mb x 64 nb tile
+  bool gemv, la, dma;  // VALU GEMV (fp32) / LDS-shared-A kernel / LDS-ring kernel (else the K-split kernel)
+  int mb, nb, S;       // k_gemm_ks: 16 mb x 16 nb tile; k_gemm_la, k_gemm_dma: 16 mb x 64 nb tile
 };
+#ifndef FC_GEMM_DMA
+#define FC_GEMM_DMA 1
+#endif
 // Tile shape and K split by typical row count, from sweeps on MI355X at the
 // engine's shapes (N = 1536 / 4608 / 6144 / 65536, K = 1536 / 6144).
 static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
@@ -722,11 +861,18 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     p.nb = 4;
     p.S = std::min(3, s_max);
   } else if (Mtyp >= 128 && N % 128 == 0) {
-    // verify / prefill rows: A shared through LDS, 128-column tiles; a wide
-    // output (lm_head) also takes 128-row tiles
-    p.la = true;
-    p.mb = N >= 16384 ? 8 : 2;
-    p.nb = 2;
+    // verify / prefill rows: a wide output (lm_head) takes the LDS-shared
+    // kernel's 128 x 128 tiles; the layer GEMMs the LDS-ring kernel's 64 x 64
+    // (the fused QKV epilogue takes its 32 x 128: one head per tile)
+    if (N >= 16384 || !FC_GEMM_DMA) {
+      p.la = true;
+      p.mb = N >= 16384 ? 8 : 2;
+      p.nb = 2;
+    } else {
+      p.dma = true;
+      p.mb = 4;
+      p.nb = 1;
+    }
     return p;
   } else {
     p.mb = 2;
@@ -740,7 +886,7 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
 bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
   if (dtype != FC_BF16 || head_dim != 128 || N % 128 != 0 || K % 64 != 0) return false;
   const GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
-  return p.la && p.mb == 2 && p.nb == 2;
+  return p.dma || (p.la && p.mb == 2 && p.nb == 2);  // the QKV tile itself is k_gemm_la's 32 x 128
 }
 
 // The EPI_ADD GEMM that writes the bf16 copy of x (attention c_proj, bf16):
@@ -799,6 +945,8 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   }
   if (p.gemv) {
     launch_gemv<float>(A, W, Mcap, Mdev, N, K, ee, s);
+  } else if (p.dma) {
+    launch_dma<4, 1>(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.la) {
     if (p.mb == 8) launch_la<8, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
     else launch_la<2, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
