@@ -64,8 +64,8 @@ class FcSpecState(Structure):
 
 EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forward", "fc_gemm", "fc_pack_operand",
            "fc_attention_workspace_bytes", "fc_attention", "fc_row_stats", "fc_spec_workspace_bytes",
-           "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_graph_begin",
-           "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
+           "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_engine_sample",
+           "fc_graph_begin", "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
 
 _lib = None
 
@@ -100,6 +100,8 @@ def _declare(L):
     L.fc_spec_part_bytes.restype = i64
     L.fc_fast_sample.argtypes = [vp, i32, i32, f32, i32, c_uint64, i32, vp, i32, vp, vp, vp, vp, vp, vp, vp]
     L.fc_fast_sample.restype = i32
+    L.fc_engine_sample.argtypes = [vp, i32, i32, f32, i32, c_uint64, vp, vp, i32, vp, vp, vp, vp, vp]
+    L.fc_engine_sample.restype = i32
     L.fc_graph_begin.argtypes = [vp]
     L.fc_graph_begin.restype = i32
     L.fc_graph_end.argtypes = [vp, POINTER(c_void_p)]

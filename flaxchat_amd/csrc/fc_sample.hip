@@ -1118,41 +1118,53 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
 }
 
 // ---------------------------------------------------------------------------
-// generate_fast sampling step (flaxchat/engine.py:308-324, 343-368)
+// generate_fast sampling step (flaxchat/engine.py:308-324, 343-368) and
+// Engine.generate's per-step token choice (flaxchat/engine.py:666-683, 773-790)
 // ---------------------------------------------------------------------------
+// ENGINE = false: rows stop on eos or at max_pos (done[] / max_pos[]).
+// ENGINE = true: no stop (completion is decided by the caller); a row with
+// forced[b] >= 0 takes that token instead of a sample.
+template <bool ENGINE>
 __global__ __launch_bounds__(NTHR) void k_fast_sample(const float* __restrict__ logits, int V, float T, int top_k,
                                                       uint64_t seed, int eos, int* __restrict__ gen, int gen_cap,
                                                       int* __restrict__ pos, int* __restrict__ done,
                                                       int* __restrict__ step, const int* __restrict__ max_pos,
-                                                      int* __restrict__ tok_cur, fc_rowstat* __restrict__ stats) {
+                                                      const int* __restrict__ forced, int* __restrict__ tok_cur,
+                                                      fc_rowstat* __restrict__ stats) {
   __shared__ StatSmem sm;
   const int b = blockIdx.x;
-  if (done[b] || pos[b] >= max_pos[b]) return;
-  const float* z = logits + (int64_t)b * V;
-  row_stats_block(z, V, T, top_k, stats + b, sm);
-  int tok;
-  const fc_rowstat rs = sm.res;
-  if (T > 0.f) {
-    const uint32_t tk = mono(rs.tau);
-    const int rnd = step[b];
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    const int ngrp = (V + 3) >> 2;
-    for (int gi = threadIdx.x; gi < ngrp; gi += NTHR) {
-      const u32x4 r = philox4x32_10(u32x4{(uint32_t)gi, (uint32_t)b, (uint32_t)rnd, 0u}, (uint32_t)seed,
-                                    (uint32_t)(seed >> 32));
+  int tok = -1;
+  if (ENGINE) {
+    tok = forced[b];
+  } else if (done[b] || pos[b] >= max_pos[b]) {
+    return;
+  }
+  if (tok < 0) {
+    const float* z = logits + (int64_t)b * V;
+    row_stats_block(z, V, T, top_k, stats + b, sm);
+    const fc_rowstat rs = sm.res;
+    if (T > 0.f) {
+      const uint32_t tk = mono(rs.tau);
+      const int rnd = step[b];
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      const int ngrp = (V + 3) >> 2;
+      for (int gi = threadIdx.x; gi < ngrp; gi += NTHR) {
+        const u32x4 r = philox4x32_10(u32x4{(uint32_t)gi, (uint32_t)b, (uint32_t)rnd, 0u}, (uint32_t)seed,
+                                      (uint32_t)(seed >> 32));
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const int i = gi * 4 + w;
-        if (i >= V) break;
-        if (!kept(z[i], i, tk, rs.tie_idx)) continue;
-        argmax_merge(bv, bi, z[i] / T + gumbel_of(pick(r, w)), i);
+        for (int w = 0; w < 4; ++w) {
+          const int i = gi * 4 + w;
+          if (i >= V) break;
+          if (!kept(z[i], i, tk, rs.tie_idx)) continue;
+          argmax_merge(bv, bi, z[i] / T + gumbel_of(pick(r, w)), i);
+        }
       }
+      block_argmax(bv, bi, sm.redv, sm.redi);
+      tok = bi;
+    } else {
+      tok = rs.argmax;
     }
-    block_argmax(bv, bi, sm.redv, sm.redi);
-    tok = bi;
-  } else {
-    tok = rs.argmax;
   }
   if (threadIdx.x == 0) {
     const int p = pos[b] + 1;
@@ -1160,7 +1172,7 @@ __global__ __launch_bounds__(NTHR) void k_fast_sample(const float* __restrict__ 
     pos[b] = p;
     tok_cur[b] = tok;
     step[b] += 1;
-    if (tok == eos) done[b] = 1;
+    if (!ENGINE && tok == eos) done[b] = 1;
   }
 }
 
@@ -1170,8 +1182,19 @@ extern "C" int32_t fc_fast_sample(const float* logits, int32_t batch, int32_t V,
                                   fc_rowstat* stats, void* stream) {
   FC_CHECK_ARG(logits && gen && pos && done && step && max_pos && tok_cur && stats, "null pointer");
   FC_CHECK_ARG(batch > 0 && V > 0 && gen_cap > 0, "sizes");
-  hipLaunchKernelGGL(k_fast_sample, dim3(batch), dim3(NTHR), 0, (hipStream_t)stream, logits, V, temperature, top_k,
-                     seed, eos, gen, gen_cap, pos, done, step, max_pos, tok_cur, stats);
+  hipLaunchKernelGGL(k_fast_sample<false>, dim3(batch), dim3(NTHR), 0, (hipStream_t)stream, logits, V, temperature,
+                     top_k, seed, eos, gen, gen_cap, pos, done, step, max_pos, nullptr, tok_cur, stats);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
+
+extern "C" int32_t fc_engine_sample(const float* logits, int32_t batch, int32_t V, float temperature, int32_t top_k,
+                                    uint64_t seed, const int32_t* forced, int32_t* gen, int32_t gen_cap, int32_t* pos,
+                                    int32_t* step, int32_t* tok_cur, fc_rowstat* stats, void* stream) {
+  FC_CHECK_ARG(logits && forced && gen && pos && step && tok_cur && stats, "null pointer");
+  FC_CHECK_ARG(batch > 0 && V > 0 && gen_cap > 0, "sizes");
+  hipLaunchKernelGGL(k_fast_sample<true>, dim3(batch), dim3(NTHR), 0, (hipStream_t)stream, logits, V, temperature,
+                     top_k, seed, -1, gen, gen_cap, pos, nullptr, step, nullptr, forced, tok_cur, stats);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

@@ -7,6 +7,10 @@ surface (flaxchat/engine.py:259-260, 410-411, 877-908).
                   seed=42, eos_token=0)
     generate_with_cache(model, tokens, max_tokens=256, temperature=1.0,
                         top_k=40, seed=42)
+    Engine(model, tokenizer).generate(tokens, num_samples=1, max_tokens=None,
+                                      temperature=1.0, top_k=40, seed=42)
+        (streaming, with the calculator tool's forced output tokens;
+        also generate_batch / generate_text)
 
 `model` / `draft_model` are host GPT containers (flaxchat_amd.gpt.GPT, the
 reference's parameter tree) or DeviceModel instances. `tokens` is a list of
@@ -22,15 +26,25 @@ Differences from the reference, by design:
     (flaxchat/engine.py:573), whose stale cache entry is reproduced and
     later repaired exactly when the reference's re-prefill would repair it;
   * cache overflow raises instead of clamping (engine.py:121-126);
-  * temperature < 0 behaves as greedy.
+  * temperature < 0 behaves as greedy;
+  * Engine.generate with max_tokens=None stops after 256 steps (the
+    reference's cache ends there and later writes are clamped); a Python
+    block the calculator cannot evaluate goes to the Engine's
+    code_executor (the reference calls its sandbox, flaxchat/execution.py;
+    pass flaxchat.execution.execute_code to get the same behaviour), and
+    without one its result is "Error".
 """
 
 from __future__ import annotations
 
+import ast
 import ctypes
+import operator
+import re
 import weakref
 from collections import deque
-from typing import List, Optional, Sequence, Union
+from dataclasses import dataclass, field
+from typing import Callable, Iterator, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
@@ -451,13 +465,299 @@ def generate_with_cache(model, tokens, max_tokens=256, temperature=1.0, top_k=40
     return out[0] if single else out
 
 
-class Engine:
-    """The reference Engine's decode entry points (flaxchat/engine.py:877-908)."""
+# ---------------------------------------------------------------------------
+# Calculator tool and per-row tool-use state (flaxchat/engine.py:614-658)
+# ---------------------------------------------------------------------------
+_CALC_CHARS = frozenset("0123456789*+-/.() ")
+_CALC_OPS = {ast.Add: operator.add, ast.Sub: operator.sub, ast.Mult: operator.mul, ast.Div: operator.truediv,
+             ast.FloorDiv: operator.floordiv, ast.Mod: operator.mod}
+# 'literal'.count('literal'): letters/digits/underscore/space in the string,
+# one word in the argument (the form flaxchat/engine.py:636-640 accepts)
+_COUNT_FORM = re.compile(r"""['"]([\w\s]+)['"]\s*\.\s*count\s*\(\s*['"](\w+)['"]\s*\)""")
 
-    def __init__(self, model, tokenizer=None, *, dtype=None, device=None):
+
+def _calc_node(node):
+    if isinstance(node, ast.Expression):
+        return _calc_node(node.body)
+    if isinstance(node, ast.Constant):
+        return node.value
+    if isinstance(node, ast.UnaryOp) and isinstance(node.op, ast.USub):
+        return -_calc_node(node.operand)
+    if isinstance(node, ast.BinOp) and type(node.op) in _CALC_OPS:
+        return _CALC_OPS[type(node.op)](_calc_node(node.left), _calc_node(node.right))
+    raise ValueError("not a calculator expression")
+
+
+def use_calculator(expr: str):
+    """The reference's calculator tool (flaxchat/engine.py:614-643): commas
+    are dropped; an expression of digits, + - * / // ( ) . and spaces (no
+    ``**``) is evaluated by walking its syntax tree (numbers, unary minus and
+    the binary operators only; nothing is compiled or executed), or
+    ``'text'.count('word')`` is counted. Anything else, or an arithmetic
+    error, gives None."""
+    expr = expr.replace(",", "")
+    if all(ch in _CALC_CHARS for ch in expr):
+        if "**" in expr:
+            return None
+        try:
+            return _calc_node(ast.parse(expr, mode="eval"))
+        except Exception:
+            return None
+    m = _COUNT_FORM.fullmatch(expr)
+    if m:
+        return m.group(1).count(m.group(2))
+    return None
+
+
+@dataclass
+class RowState:
+    """Per-row state of Engine.generate (flaxchat/engine.py:649-658)."""
+    current_tokens: List[int] = field(default_factory=list)
+    forced_tokens: deque = field(default_factory=deque)
+    in_python_block: bool = False
+    python_expr_tokens: List[int] = field(default_factory=list)
+    completed: bool = False
+
+
+class ToolUse:
+    """Host side of Engine.generate's tool protocol
+    (flaxchat/engine.py:742-749, 786-822): the special token ids, and the
+    transition of one row on its next token: completion on assistant_end or
+    bos; tokens between python_start and python_end are decoded and
+    evaluated (calculator, then `code_executor`), and the result is queued
+    as output_start + tokens + output_end."""
+
+    def __init__(self, tokenizer, code_executor: Optional[Callable] = None):
+        sp = tokenizer.encode_special
+        self.tokenizer = tokenizer
+        self.python_start, self.python_end = sp("<|python_start|>"), sp("<|python_end|>")
+        self.output_start, self.output_end = sp("<|output_start|>"), sp("<|output_end|>")
+        self.assistant_end = sp("<|assistant_end|>")
+        self.bos = tokenizer.get_bos_token_id()
+        self.code_executor = code_executor
+
+    def evaluate(self, expr: str) -> str:
+        result = use_calculator(expr)
+        if result is not None:
+            return str(result)
+        if self.code_executor is not None:
+            r = self.code_executor(expr)
+            if r.success:
+                return r.stdout.rstrip("\n")
+        return "Error"
+
+    def next_token(self, state: RowState, sampled: int) -> Tuple[int, int]:
+        """The row's token for this step (the head of its forced queue, else
+        `sampled`) and its mask (0 forced, 1 sampled); updates the state."""
+        forced = len(state.forced_tokens) > 0
+        tok = state.forced_tokens.popleft() if forced else int(sampled)
+        state.current_tokens.append(tok)
+        if tok == self.assistant_end or tok == self.bos:
+            state.completed = True
+        if tok == self.python_start:
+            state.in_python_block = True
+            state.python_expr_tokens = []
+        elif tok == self.python_end and state.in_python_block:
+            state.in_python_block = False
+            if state.python_expr_tokens:
+                out = self.tokenizer.encode(self.evaluate(self.tokenizer.decode(state.python_expr_tokens)))
+                state.forced_tokens.append(self.output_start)
+                state.forced_tokens.extend(int(t) for t in out)
+                state.forced_tokens.append(self.output_end)
+            state.python_expr_tokens = []
+        elif state.in_python_block:
+            state.python_expr_tokens.append(tok)
+        return tok, 0 if forced else 1
+
+
+class StreamSession:
+    """Device state of Engine.generate (flaxchat/engine.py:686-838): the
+    prompt is prefilled once and copied into `num_samples` rows; each step
+    picks a forced or sampled token per row on the device (fc_engine_sample),
+    copies the column to the host, and feeds it, so the next forward runs
+    while the host applies the tool protocol to this column."""
+
+    def __init__(self, dm: DeviceModel, tokens: List[int], num_samples: int, steps: int, temperature: float,
+                 top_k: Optional[int], seed: int, use_graph: bool = True, stream=None):
+        _check_rows([tokens], dm.V)
+        if num_samples < 1:
+            raise ValueError("num_samples must be >= 1")
+        self.dm, self.tokens = dm, list(tokens)
+        self.B = B = int(num_samples)
+        self.temperature = float(temperature)
+        self.top_k = min(int(top_k), dm.V) if top_k is not None and top_k > 0 else 0
+        self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+        self.use_graph = use_graph
+        dev = dm.device
+        self.stream = stream or torch.cuda.Stream(device=dev)
+        P = len(tokens)
+        self.cap = P + int(steps) + 8
+        if self.cap > dm.t["rope_cos"].shape[0]:
+            raise ValueError("sequence exceeds the RoPE table")
+        i32 = dict(dtype=torch.int32, device=dev)
+        with torch.cuda.stream(self.stream):
+            self.cache = DeviceCache(dm, B, self.cap)
+            self.gen = torch.zeros(B, self.cap, **i32)
+            self.pos = torch.full((B,), P - 1, **i32)
+            self.step = torch.zeros(B, **i32)
+            self.tok = torch.full((B,), int(tokens[-1]), **i32)
+            self.forced = torch.full((B,), -1, **i32)
+            self.row_off = torch.arange(B + 1, **i32)
+            self.logits = torch.zeros(B, dm.V, dtype=torch.float32, device=dev)
+            self.stats = torch.zeros(B * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev)
+        self.forced_host = torch.full((B,), -1, dtype=torch.int32).pin_memory()
+        self.tok_host = torch.zeros(B, dtype=torch.int32).pin_memory()
+        self.event = torch.cuda.Event()
+        self.ws = Workspace(dev)
+        self.ws_pre = Workspace(dev)
+        nb = lib().fc_forward_workspace_bytes(ctypes.byref(dm.desc), B, B, 1, B)
+        with torch.cuda.stream(self.stream):
+            self.ws.get(nb)
+        self.graph = None
+        self.forwards = 0
+
+    def _forward(self):
+        forward_packed(self.dm, self.cache, self.tok, self.row_off, self.pos, 1, 1, self.logits, self.ws,
+                       self.stream.cuda_stream)
+
+    def _launch_forward(self):
+        s = self.stream.cuda_stream
+        if self.graph is not None:
+            check(lib().fc_graph_launch(self.graph, s), "fc_graph_launch")
+        elif self.use_graph and self.forwards >= 1:
+            check(lib().fc_graph_begin(s), "fc_graph_begin")
+            try:
+                self._forward()
+            finally:
+                ex = ctypes.c_void_p()
+                rc = lib().fc_graph_end(s, ctypes.byref(ex))
+            check(rc, "fc_graph_end")
+            self.graph = ex
+            check(lib().fc_graph_launch(self.graph, s), "fc_graph_launch")
+        else:
+            self._forward()
+        self.forwards += 1
+
+    def prefill(self):
+        """Prefill row 0 with the prompt, copy its cache into every row, and
+        compute the logits after the last prompt token."""
+        with torch.cuda.stream(self.stream):
+            prefill_rows(self.dm, self.cache, [self.tokens[:-1]] + [[]] * (self.B - 1), [0] * self.B, self.ws_pre)
+            c = self.cache
+            if self.B > 1:
+                c.k[:, 1:] = c.k[:, :1]
+                c.v[:, 1:] = c.v[:, :1]
+                c.hist[1:] = c.hist[:1]
+            self.gen[:, :len(self.tokens)] = torch.tensor(self.tokens, dtype=torch.int32, device=self.gen.device)
+            self._launch_forward()
+
+    def next_column(self, forced: Sequence[int]) -> List[int]:
+        """One column: row b takes forced[b] when >= 0, else a sample; the
+        forward of the chosen column is queued before this returns."""
+        self.forced_host.numpy()[:] = forced
+        s = self.stream.cuda_stream
+        with torch.cuda.stream(self.stream):
+            self.forced.copy_(self.forced_host, non_blocking=True)
+            check(lib().fc_engine_sample(self.logits.data_ptr(), self.B, self.dm.V, self.temperature, self.top_k,
+                                         self.seed, self.forced.data_ptr(), self.gen.data_ptr(), self.cap,
+                                         self.pos.data_ptr(), self.step.data_ptr(), self.tok.data_ptr(),
+                                         self.stats.data_ptr(), s), "fc_engine_sample")
+            self.tok_host.copy_(self.tok, non_blocking=True)
+            self.event.record(self.stream)
+            self._launch_forward()
+        self.event.synchronize()
+        return self.tok_host.numpy().tolist()
+
+    def close(self):
+        if self.graph is not None:
+            lib().fc_graph_destroy(self.graph)
+            self.graph = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Engine:
+    """The reference Engine (flaxchat/engine.py:661-908): streaming
+    generation with tool use, and the fast / speculative decode entry points.
+    `code_executor(code) -> result with .success and .stdout` runs Python
+    blocks the calculator cannot (the reference's sandboxed execute_code,
+    flaxchat/execution.py:190)."""
+
+    def __init__(self, model, tokenizer=None, *, dtype=None, device=None, code_executor=None):
         self.model = model
         self.tokenizer = tokenizer
         self.dtype, self.device = dtype, device
+        self.code_executor = code_executor
+
+    def generate(self, tokens, num_samples=1, max_tokens=None, temperature=1.0, top_k=40,
+                 seed=42) -> Iterator[Tuple[List[int], List[int]]]:
+        """Yields (token_column, token_masks) per step, one entry per sample
+        (flaxchat/engine.py:686-838): 1 = sampled, 0 = forced tool output.
+        Stops after max_tokens steps (256 when None) or when every row has
+        emitted assistant_end or bos; completed rows keep sampling until
+        then, as in the reference."""
+        assert isinstance(tokens, list) and isinstance(tokens[0], int), "expecting list of ints"
+        assert temperature >= 0.0, "temperature must be non-negative"
+        if self.tokenizer is None:
+            raise ValueError("Engine.generate needs a tokenizer (special tokens of the tool protocol)")
+        tool = ToolUse(self.tokenizer, self.code_executor)
+        dm = as_device_model(self.model, self.dtype, self.device)
+        steps = 256 if max_tokens is None else int(max_tokens)
+        if steps <= 0:
+            return
+        sess = StreamSession(dm, tokens, num_samples, steps, temperature, top_k, seed)
+        rows = [RowState(list(tokens)) for _ in range(num_samples)]
+        try:
+            sess.prefill()
+            for _ in range(steps):
+                if all(r.completed for r in rows):
+                    break
+                forced = [r.forced_tokens[0] if r.forced_tokens else -1 for r in rows]
+                for f in forced:
+                    if f >= dm.V:
+                        raise ValueError(f"tool output token {f} is outside the vocabulary ({dm.V})")
+                sampled = sess.next_column(forced)
+                column, masks = [], []
+                for r, t in zip(rows, sampled):
+                    tok, mask = tool.next_token(r, t)
+                    column.append(tok)
+                    masks.append(mask)
+                yield column, masks
+        finally:
+            sess.close()
+
+    def generate_batch(self, tokens, num_samples=1, **kwargs):
+        """Final sequences and masks (flaxchat/engine.py:840-864): prompt
+        plus generated tokens up to, not including, assistant_end / bos;
+        mask 0 for prompt and forced tokens, 1 for sampled ones."""
+        tool_end = self.tokenizer.encode_special("<|assistant_end|>")
+        bos = self.tokenizer.get_bos_token_id()
+        results = [list(tokens) for _ in range(num_samples)]
+        masks = [[0] * len(tokens) for _ in range(num_samples)]
+        completed = [False] * num_samples
+        for column, cmask in self.generate(tokens, num_samples, **kwargs):
+            for i, (tok, m) in enumerate(zip(column, cmask)):
+                if completed[i]:
+                    continue
+                if tok == tool_end or tok == bos:
+                    completed[i] = True
+                else:
+                    results[i].append(tok)
+                    masks[i].append(m)
+            if all(completed):
+                break
+        return results, masks
+
+    def generate_text(self, prompt, max_tokens=256, temperature=1.0, top_k=40, seed=42):
+        """Decoded text of one streamed sample (flaxchat/engine.py:866-874)."""
+        tokens = self.tokenizer(prompt, prepend="<|bos|>")
+        results, _ = self.generate_batch(tokens, num_samples=1, max_tokens=max_tokens, temperature=temperature,
+                                         top_k=top_k, seed=seed)
+        return self.tokenizer.decode(results[0])
 
     def generate_fast(self, tokens, max_tokens=256, temperature=1.0, top_k=40, seed=42, eos_token=0):
         return generate_fast(self.model, tokens, max_tokens=max_tokens, temperature=temperature, top_k=top_k,

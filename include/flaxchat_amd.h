@@ -240,6 +240,20 @@ int32_t fc_fast_sample(const float* logits, int32_t batch, int32_t V, float temp
                        int32_t* pos, int32_t* done, int32_t* step, const int32_t* max_pos,
                        int32_t* tok_cur, fc_rowstat* stats, void* stream);
 
+/* Engine.generate's token choice for one step (flaxchat/engine.py:666-683
+ * sampling, :773-790 forced-or-sampled selection). For every row b:
+ * forced[b] >= 0 takes that token (a tool-output token the caller queued;
+ * the caller guarantees forced[b] < V); otherwise sample from logits row b
+ * exactly as fc_fast_sample (argmax when temperature <= 0; top_k <= 0 keeps
+ * the whole vocabulary; Philox counter (group, b, step[b])). The token is
+ * written at gen[b][pos[b]+1] and tok_cur[b]; pos and step advance. Rows
+ * never stop here: the reference's completion (assistant_end / bos) is the
+ * caller's bookkeeping. */
+int32_t fc_engine_sample(const float* logits, int32_t batch, int32_t V, float temperature,
+                         int32_t top_k, uint64_t seed, const int32_t* forced, int32_t* gen,
+                         int32_t gen_cap, int32_t* pos, int32_t* step, int32_t* tok_cur,
+                         fc_rowstat* stats, void* stream);
+
 /* Stream capture into a replayable hipGraph (the captured draft loop). */
 int32_t fc_graph_begin(void* stream);
 int32_t fc_graph_end(void* stream, void** exec_out);

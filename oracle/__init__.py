@@ -17,6 +17,9 @@ Modules:
             (the engine's chunked verify + length-pointer rollback state
             machine); generate_fast (engine.py:259-376) and
             generate_with_cache (engine.py:209-253).
+  engine_stream  Engine.generate (engine.py:686-838): the streaming loop
+            with per-row tool-use state, forced tokens and the calculator
+            tool (engine.py:614-643).
 
 Pinning (what checks each function, beyond restating the reference):
   * philox: Random123 known-answer vectors (tests/test_oracle.py).
@@ -34,4 +37,9 @@ Pinning (what checks each function, beyond restating the reference):
     reference); generate_fast greedy == generate_with_cache greedy
     (reference tests/test_engine.py:94-103); chi-square of the first
     emitted token against the target distribution.
+  * engine_stream: the calculator against the reference's own test cases
+    (tests/test_engine.py:153-171 of the reference) plus hand-worked
+    expressions; the tool state machine against hand-worked token
+    sequences (a python block, the forced output, completion); greedy
+    streaming without tool tokens == generate_with_cache greedy.
 """
