@@ -14,7 +14,11 @@
 //              steps and the split-K residual GEMMs.
 //   k_gemm_la  bf16 MFMA, 32-128 rows x 128 columns, the four waves split
 //              the columns and share the activation tile through LDS;
-//              verify / prefill row counts and the verify lm_head.
+//              verify row counts and the verify lm_head.
+//   k_gemm_dma bf16 MFMA, 64 x 64 tiles fed by direct global-to-LDS loads
+//              into a 4-stage ring; verify c_fc.
+//   k_gemm_big bf16 MFMA, 256 x 256 tiles, 4-stage LDS ring of direct
+//              loads; prefill chunks (M >= 1024).
 // The row count may be a device value (packed token chunks whose size is
 // only known on the GPU): the grid covers the capacity and tiles past the
 // actual count exit at once.
@@ -744,6 +748,239 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
   tile_epilogue<MB, NBW, EPI>(e, acc, rpre, m0, n0, nt, 0, M, K);
 }
 
+// bf16 MFMA GEMM for prefill-size row counts (M >= FC_BIG_M, N % 256 == 0,
+// K % 128 == 0).
+//
+// A workgroup owns a 256 x 256 output tile; each of its four waves owns a
+// 128 x 128 quadrant as 4 x 4 blocks of 32 x 32 (the 32x32x16 MFMA: with
+// one wave per SIMD it keeps the matrix unit ~86% busy, where 16x16x32
+// chains reach about half), 256 accumulators per lane. Per 32-wide k step
+// the tile needs 16 activation and 16 weight blocks of 1 KB (16 rows x 32 k,
+// fragment order); they go straight from global memory into one of four
+// 32 KB LDS stages by direct loads, 8 per wave. The 32x32x16 operand of
+// lane l is row l % 32, k 8 (l / 32) .. +7 of a 16-k half: 16 bytes that sit
+// in 16-row block (l % 32) / 16 at lane slot l % 16 + 16 (2 half + l / 32),
+// so the stored layout feeds it unchanged.
+//
+// Per step i: wait until stage i+1 has landed (own loads: vmcnt(16), the two
+// later stages may still be in flight) and every wave has finished reading
+// stage i into registers (lgkmcnt(0)); one barrier; start reading stage i+1
+// into the other fragment set; refill stage i with chunk i+4; then the 32
+// MFMAs of step i run on fragments already in registers.
+//
+// The MFMA takes the weight block as its first operand, so a lane's result
+// is row m0 + l % 32 and, per group of four registers, four consecutive
+// columns: fp32 outputs are written as float4, and the bf16 fragment-order
+// output (ReLU^2, the next GEMM's operand) goes through a 32 x 32 LDS
+// transpose per wave (8-byte writes, 16-byte reads).
+//
+// Tile order: tiles are grouped by 4 M tiles (N tile slower within a group)
+// and dealt to the eight XCDs in contiguous ranges, so the ~32 workgroups
+// an XCD runs at once cover about 4 M tiles x 8 N tiles and share their
+// operand slabs in that XCD's L2.
+#ifndef FC_BIG_M
+#define FC_BIG_M 1024
+#endif
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 mfma32(v4u a, v4u b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+}
+struct BigStage {
+  uint4 a[16][64];
+  uint4 w[16][64];
+};
+template <int EPI>
+__device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0, float v1, float v2, float v3) {
+  if constexpr (EPI == EPI_STORE) {
+    *(float4*)((float*)e.out + (int64_t)m * e.ldo + n) = float4{v0, v1, v2, v3};
+  } else if constexpr (EPI == EPI_ADD) {
+    float4* o = (float4*)((float*)e.out + (int64_t)m * e.ldo + n);
+    const float4 x = *o;
+    *o = float4{x.x + v0, x.y + v1, x.z + v2, x.w + v3};
+  } else if constexpr (EPI == EPI_MLPOUT) {
+    const int64_t i = (int64_t)m * e.ldo + n;
+    float4* xp = (float4*)((float*)e.out + i);
+    const float4 x = *xp;
+    const float4 t = float4{x.x + v0, x.y + v1, x.z + v2, x.w + v3};  // engine.py:161
+    float4 xb = float4{0.f, 0.f, 0.f, 0.f};
+    if (e.capture) {                                                   // engine.py:164
+      *(float4*)(e.xb + i) = t;
+      xb = t;
+    } else if (e.last) {
+      xb = *(const float4*)(e.xb + i);
+    }
+    if (e.last) {                                                      // engine.py:166
+      *xp = float4{t.x - e.lb * xb.x, t.y - e.lb * xb.y, t.z - e.lb * xb.z, t.w - e.lb * xb.w};
+    } else {                                                           // engine.py:94
+      const float4 x0 = *(const float4*)(e.x0 + i);
+      *xp = float4{e.r * t.x + e.a * x0.x, e.r * t.y + e.a * x0.y, e.r * t.z + e.a * x0.z, e.r * t.w + e.a * x0.w};
+    }
+  } else {
+    epi_apply<EPI>(e, m, n, v0);
+    epi_apply<EPI>(e, m, n + 1, v1);
+    epi_apply<EPI>(e, m, n + 2, v2);
+    epi_apply<EPI>(e, m, n + 3, v3);
+  }
+}
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                  int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
+                                                  int mtiles, int per_xcd, Epi e) {
+  constexpr int NSTG = 4, GM = 4;
+  __shared__ BigStage s0, s1, s2, s3;
+  // tile of this workgroup: XCD id % 8 takes grouped tiles [x per_xcd, (x + 1) per_xcd)
+  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= per_xcd || t >= ntiles * mtiles) return;
+  const int grp = t / (GM * ntiles), rr = t - grp * GM * ntiles;
+  const int gm = min(GM, mtiles - grp * GM);
+  const int nt = rr / gm, mt = grp * GM + rr % gm;
+  const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
+  const int m0 = mt * 256;
+  if (m0 >= M) return;
+  const int n0 = nt * 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t KS32 = K >> 5;
+  const int C = K >> 5;
+  const int last_blk = (M - 1) >> 4;
+  // this wave's loads: activation row blocks 4 wave .. +3 and weight column blocks 4 wave .. +3
+  const bf16_t* ab[4];
+  const bf16_t* wb[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ab[u] = A + (int64_t)min(m0 / 16 + 4 * wave + u, last_blk) * KS32 * 512 + lane * 8;
+    wb[u] = W + (int64_t)(n0 / 16 + 4 * wave + u) * KS32 * 512 + lane * 8;
+  }
+  // this lane's 32x32x16 operand slot: 16-row block offset and lane slot (half 0; +32 for half 1)
+  const int sub = (lane & 31) >> 4, slot = (lane & 15) + 16 * (lane >> 5);
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc[p][q][x] = 0.f;
+  constexpr int NV = 8 * (NSTG - 2);
+  static_assert(NV < 64, "vmcnt range");
+#define BIG_ISSUE(S, c_)                                                                                      \
+  {                                                                                                           \
+    const int c = min((c_), C - 1); /* past the end: harmless re-reads into an unread stage */                \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                                           \
+      __builtin_amdgcn_global_load_lds((const void*)(ab[u] + (int64_t)c * 512),                              \
+                                       (__attribute__((address_space(3))) void*)&S.a[4 * wave + u][0], 16, 0, 0); \
+      __builtin_amdgcn_global_load_lds((const void*)(wb[u] + (int64_t)c * 512),                              \
+                                       (__attribute__((address_space(3))) void*)&S.w[4 * wave + u][0], 16, 0, 0); \
+    }                                                                                                         \
+  }
+#define BIG_SYNC(NVW)                                                                                         \
+  {                                                                                                           \
+    __builtin_amdgcn_sched_barrier(0); /* the wait must not rise above the previous step's MFMAs */           \
+    __builtin_amdgcn_s_waitcnt(((NVW) & 15) | (((NVW) >> 4) << 14) | (7 << 4) | (0 << 8));                  \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                                  \
+    __builtin_amdgcn_sched_barrier(0);                                                                        \
+    __builtin_amdgcn_s_barrier();                                                                             \
+    __builtin_amdgcn_sched_barrier(0);                                                                        \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                                  \
+  }
+  // fragments of one k step: [half][32-row / 32-column block]
+#define BIG_READ(S, WF, AF)                                                                                   \
+  {                                                                                                           \
+    _Pragma("unroll") for (int h = 0; h < 2; ++h)                                                             \
+      _Pragma("unroll") for (int b = 0; b < 4; ++b) {                                                         \
+        WF[h][b] = __builtin_bit_cast(v4u, S.w[8 * wn + 2 * b + sub][slot + 32 * h]);                         \
+        AF[h][b] = __builtin_bit_cast(v4u, S.a[8 * wm + 2 * b + sub][slot + 32 * h]);                         \
+      }                                                                                                       \
+  }
+#define BIG_MMA(WF, AF)                                                                                       \
+  {                                                                                                           \
+    _Pragma("unroll") for (int h = 0; h < 2; ++h)                                                             \
+      _Pragma("unroll") for (int p = 0; p < 4; ++p)                                                           \
+        _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[p][q] = mfma32(WF[h][q], AF[h][p], acc[p][q]);      \
+  }
+  // step i: SN = stage of chunk i + 1 (read now), SI = stage of chunk i (refilled with chunk i + 4)
+#define BIG_STEP(SI, SN, WFC, AFC, WFN, AFN, i_)                                                              \
+  {                                                                                                           \
+    BIG_SYNC(NV);                                                                                             \
+    BIG_READ(SN, WFN, AFN);                                                                                   \
+    BIG_ISSUE(SI, (i_) + NSTG);                                                                               \
+    BIG_MMA(WFC, AFC);                                                                                        \
+  }
+  v4u wf0[2][4], af0[2][4], wf1[2][4], af1[2][4];
+  BIG_ISSUE(s0, 0);
+  BIG_ISSUE(s1, 1);
+  BIG_ISSUE(s2, 2);
+  BIG_ISSUE(s3, 3);
+  BIG_SYNC(3 * 8);  // chunk 0 landed
+  BIG_READ(s0, wf0, af0);
+  // C % 4 == 0 (K % 128 == 0): 4-step groups, the last one ends without a read
+  int i = 0;
+  for (; i + 4 < C; i += 4) {
+    BIG_STEP(s0, s1, wf0, af0, wf1, af1, i);
+    BIG_STEP(s1, s2, wf1, af1, wf0, af0, i + 1);
+    BIG_STEP(s2, s3, wf0, af0, wf1, af1, i + 2);
+    BIG_STEP(s3, s0, wf1, af1, wf0, af0, i + 3);
+  }
+  BIG_STEP(s0, s1, wf0, af0, wf1, af1, i);
+  BIG_STEP(s1, s2, wf1, af1, wf0, af0, i + 1);
+  BIG_STEP(s2, s3, wf0, af0, wf1, af1, i + 2);
+  BIG_MMA(wf1, af1);
+#undef BIG_STEP
+#undef BIG_MMA
+#undef BIG_READ
+#undef BIG_SYNC
+#undef BIG_ISSUE
+  __builtin_amdgcn_s_waitcnt(0);  // no direct load outlives the workgroup's LDS
+  __syncthreads();                // stage s0 becomes the epilogue's scratch
+  // lane l holds row 32 p + l % 32 of the quadrant; register 4 j + x holds
+  // column 32 q + 8 j + 4 (l / 32) + x
+  const int rl = lane & 31, ch = 4 * (lane >> 5);
+  if constexpr (EPI == EPI_RELU2) {
+    // bf16 fragment order: per 32 x 32 block, lane l writes row l % 32,
+    // columns 8 j + 4 (l / 32) .. +3 into a 32 x 80 B scratch; then per
+    // 16-row half, lane L reads row L % 16, columns 8 (L / 16) .. +7
+    char* scr = (char*)&s0 + wave * 32 * 80;
+    bf16_t* out = (bf16_t*)e.out;
+    const int KB = e.ldo >> 5;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t pk[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float x0 = fmaxf(acc[p][q][4 * j + 2 * hh], 0.f), x1 = fmaxf(acc[p][q][4 * j + 2 * hh + 1], 0.f);
+            pk[hh] = (uint32_t)f2bf(x0 * x0) | ((uint32_t)f2bf(x1 * x1) << 16);
+          }
+          *(uint2*)(scr + rl * 80 + (8 * j + ch) * 2) = uint2{pk[0], pk[1]};
+        }
+        const int kb = (n0 + 128 * wn + 32 * q) >> 5;
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+          const uint4 val = *(const uint4*)(scr + (16 * hs + (lane & 15)) * 80 + 16 * (lane >> 4));
+          const int rb = (m0 + 128 * wm + 32 * p + 16 * hs) >> 4;
+          if (16 * rb < M) *(uint4*)(out + ((int64_t)rb * KB + kb) * 512 + lane * 8) = val;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int m = m0 + 128 * wm + 32 * p + rl;
+      if (m < M) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            big_store4<EPI>(e, m, n0 + 128 * wn + 32 * q + 8 * j + ch, acc[p][q][4 * j], acc[p][q][4 * j + 1],
+                            acc[p][q][4 * j + 2], acc[p][q][4 * j + 3]);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Dispatch
 // ---------------------------------------------------------------------------
@@ -808,6 +1045,25 @@ static void launch_dma(const void* A, const void* W, int Mcap, const int* Mdev, 
                                            (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, mtiles, mfast, e));
 }
 
+template <int EPI>
+static void launch_big_e(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
+                         hipStream_t s) {
+  const int ntiles = N / 256, mtiles = (Mcap + 255) / 256;
+  const int per_xcd = (ntiles * mtiles + 7) / 8;
+  hipLaunchKernelGGL((k_gemm_big<EPI>), dim3(8 * per_xcd), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W, Mcap,
+                     Mdev, N, K, ntiles, mtiles, per_xcd, e);
+}
+static void launch_big(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
+                       hipStream_t s) {
+  switch (e.mode) {
+    case EPI_STORE: launch_big_e<EPI_STORE>(A, W, Mcap, Mdev, N, K, e, s); break;
+    case EPI_ADD: launch_big_e<EPI_ADD>(A, W, Mcap, Mdev, N, K, e, s); break;
+    case EPI_RELU2: launch_big_e<EPI_RELU2>(A, W, Mcap, Mdev, N, K, e, s); break;
+    case EPI_MLPOUT: launch_big_e<EPI_MLPOUT>(A, W, Mcap, Mdev, N, K, e, s); break;
+    default: launch_big_e<EPI_SOFTCAP>(A, W, Mcap, Mdev, N, K, e, s); break;
+  }
+}
+
 static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
                           hipStream_t s) {
   const int ntiles = N / 128, mtiles = (Mcap + 31) / 32;
@@ -820,7 +1076,7 @@ static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mde
 // the K split are chosen for the typical row count Mtyp (the grid covers
 // Mcap rows; tiles past the device-side count exit at once).
 struct GemmPlan {
-  bool gemv, la, dma;  // VALU GEMV (fp32) / LDS-shared-A kernel / LDS-ring kernel (else the K-split kernel)
+  bool gemv, la, dma, big;  // VALU GEMV (fp32) / LDS-shared-A / LDS-ring / 256 x 256 (else the K-split kernel)
   int mb, nb, S;       // k_gemm_ks: 16 mb x 16 nb tile; k_gemm_la, k_gemm_dma: 16 mb x 64 nb tile
 };
 #ifndef FC_GEMM_DMA
@@ -833,6 +1089,10 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
   p.S = 1;
   if (dtype == FC_F32) {
     p.gemv = true;
+    return p;
+  }
+  if (Mtyp >= FC_BIG_M && N % 256 == 0 && K % 128 == 0) {  // prefill chunks: 256 x 256 tiles, MFMA-bound
+    p.big = true;
     return p;
   }
   const int C = K / 64;
@@ -905,7 +1165,7 @@ int fc_gemm_fold_tiles(int Mtyp, int N) { return N / (16 * plan_fold_add(Mtyp, N
 // with 256 / MT threads per row
 bool fc_gemm_fold_ok(int Mtyp, int D) {
   const GemmPlan c = plan_gemm(Mtyp, 4 * D, D, FC_BF16, false);
-  return !c.gemv && fc_gemm_fold_tiles(Mtyp, D) <= FC_RMS_REG * (256 / (16 * c.mb));
+  return !c.gemv && !c.big && fc_gemm_fold_tiles(Mtyp, D) <= FC_RMS_REG * (256 / (16 * c.mb));
 }
 
 int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K) {
@@ -945,6 +1205,10 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   }
   if (p.gemv) {
     launch_gemv<float>(A, W, Mcap, Mdev, N, K, ee, s);
+  } else if (p.big) {
+    FC_CHECK_ARG(ee.mode != EPI_PARTIAL && ee.rms_in == nullptr && ee.xa == nullptr,
+                 "the 256 x 256 GEMM has no split-K or folded-norm epilogue");
+    launch_big(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.dma) {
     launch_dma<4, 1>(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.la) {

@@ -17,7 +17,7 @@ torch = pytest.importorskip("torch")
 from flaxchat_amd import _lib  # noqa: E402
 from flaxchat_amd.engine import (SpecSession, generate_fast, generate_speculative,  # noqa: E402
                                  generate_with_cache, as_device_model, VocabMismatchError)
-from flaxchat_amd.runtime import DeviceCache, DeviceModel, Workspace, forward_rows  # noqa: E402
+from flaxchat_amd.runtime import DeviceCache, DeviceModel, Workspace, forward_rows, prefill_rows  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -102,6 +102,38 @@ def test_single_token_rows_bf16(cfg1_pair):
         err = max(err, np.abs(np.stack([g[b] for g in got]) - ref).max())
     _say(f"single-token rows bf16: max abs err {err:.3e}")
     assert err < 5e-2
+
+
+def test_prefill_size_chunk_bf16(cfg1_pair):
+    """A chunk of > 1024 packed tokens (the 256 x 256 GEMM tiles, unfused
+    QKV prologue, unfolded norm) against the oracle and against the same
+    rows fed in small chunks (the decode-size kernels)."""
+    _say("prefill-size chunk bf16")
+    tgt = cfg1_pair[0]
+    dm = as_device_model(tgt, "bf16")
+    rng = np.random.default_rng(9)
+    lens = [230, 256, 171, 256, 199, 250]
+    rows = [rng.integers(0, tgt.config.vocab_size, n).tolist() for n in lens]
+    B = len(rows)
+    ws = Workspace(dm.device)
+    big = DeviceCache(dm, B, 320)
+    lg_big = torch.zeros(B, 1, dm.V, device=dm.device)
+    forward_rows(dm, big, rows, [0] * B, 1, lg_big, ws)
+    small = DeviceCache(dm, B, 320)
+    lg_small = torch.zeros(B, 1, dm.V, device=dm.device)
+    prefill_rows(dm, small, [r[:-1] for r in rows], [0] * B, ws, chunk=64)  # 384-token chunks
+    forward_rows(dm, small, [r[-1:] for r in rows], [len(r) - 1 for r in rows], 1, lg_small, ws)
+    torch.cuda.synchronize()
+    a, b = lg_big.cpu().numpy()[:, 0], lg_small.cpu().numpy()[:, 0]
+    for i, r in enumerate(rows):
+        ref = _oracle_logits(tgt, r)[-1]
+        assert np.abs(a[i] - ref).max() < 5e-2, (i, np.abs(a[i] - ref).max())
+        assert np.abs(a[i] - b[i]).max() < 5e-2, (i, np.abs(a[i] - b[i]).max())
+    # the K / V cache written by both paths
+    for i, r in enumerate(rows):
+        n = len(r)
+        kb, ks = big.k[:, i, :, :n].float(), small.k[:, i, :, :n].float()
+        assert (kb - ks).abs().max().item() < 5e-2
 
 
 def test_chunk_equals_steps(cfg1_pair):
