@@ -22,6 +22,8 @@
 //                  read from the 32-key blocked-transposed V cache as one
 //                  16-byte load per lane).
 // The four waves merge in LDS; splits merge in k_attn_combine.
+// Prefill-width chunks (>= 128 query columns per row) take k_attn_chunk:
+// each wave owns 2 query blocks and reads every K/V tile once for both.
 // fp32 path (parity mode, or head_dim != 128): one workgroup per query with
 // the reference's operation order (scores, max, exp, normalise, weighted sum).
 #include "fc_common.h"
@@ -361,6 +363,118 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
   }
 }
 
+// Prefill-width chunks (many queries per row): each wave owns QB query
+// blocks of 16 columns of one (row, KV group) and walks every 32-key tile of
+// their combined key range itself, so each K/V tile is read once per QB
+// blocks (the decode kernel reads it once per block) and applied to all of
+// them from registers; no merge between waves. Two tiles are in flight per
+// wave. A block skips the tiles it cannot see (past its last position or
+// before its window). Output: normalised, in the c_proj operand layout.
+template <int QB>
+__global__ __launch_bounds__(256) void k_attn_chunk(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+                                                    const bf16_t* __restrict__ vc, bf16_t* __restrict__ y, int H,
+                                                    int G, int cap, const int* __restrict__ row_off,
+                                                    const int* __restrict__ start, int max_per_row, int Mcap,
+                                                    int window, float scale_log2) {
+  constexpr int HD = 128;
+  const int bg = blockIdx.y, b = bg / G, g = bg - b * G, rep = H / G;
+  const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
+  const int base = sp.base, n = sp.n, s0 = start[b];
+  const int ncol = n * rep;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qb0 = (blockIdx.x * 4 + wave) * QB;
+  if (qb0 * 16 >= ncol) return;  // waves work independently: no barrier below
+  const int c = lane & 15, g4 = lane >> 4;
+  // this wave's key range: from the first column's window start to the last column's position
+  const int f = qb0 * 16, lcol = min(qb0 * 16 + QB * 16 - 1, ncol - 1);
+  const int pf = s0 + f / rep, pl = s0 + lcol / rep;
+  const int kbeg = window > 0 ? max(0, pf - window) : 0;
+  const int kend = min(pl + 1, cap);
+  // per block: this lane's column, its position and window start; the block's key span
+  bool cvalid[QB];
+  int pos_c[QB], lo_c[QB], head_c[QB], j_c[QB], bhi[QB], blo[QB];
+  uint4 qf[QB][4];
+  const uint4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    const int col = (qb0 + u) * 16 + c;
+    cvalid[u] = col < ncol;
+    const int j = cvalid[u] ? col / rep : 0;
+    j_c[u] = j;
+    head_c[u] = g * rep + (col - (col / rep) * rep);
+    pos_c[u] = s0 + j;
+    lo_c[u] = window > 0 ? max(0, pos_c[u] - window) : 0;
+    const int bl = min((qb0 + u) * 16 + 15, ncol - 1), bf = min((qb0 + u) * 16, ncol - 1);
+    bhi[u] = s0 + bl / rep;  // last position any column of the block sees
+    blo[u] = window > 0 ? max(0, s0 + bf / rep - window) : 0;
+    const bf16_t* qr = q + ((int64_t)(base + j) * H + (cvalid[u] ? head_c[u] : 0)) * HD + 8 * g4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[u][s] = cvalid[u] ? *(const uint4*)(qr + 32 * s) : zero;
+  }
+  const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
+  const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
+  float m_run[QB], l_run[QB];
+  f32x4 O[QB][8];
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    m_run[u] = -INFINITY;
+    l_run[u] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) O[u][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int t0 = kbeg & ~31;
+  const int ntiles = (kend - t0 + 31) >> 5;
+#define CH_LOAD(kf, vf, kb_)                                                                       \
+  {                                                                                                \
+    const bf16_t* kt = kbase + (int64_t)((kb_) >> 5) * 32 * HD + lane * 8;                         \
+    _Pragma("unroll") for (int cc = 0; cc < 2; ++cc)                                               \
+      _Pragma("unroll") for (int s = 0; s < 4; ++s) kf[cc][s] = KV_LD((const uint4*)(kt + (s * 2 + cc) * 512)); \
+    const bf16_t* vt = vbase + (int64_t)((kb_) >> 5) * HD * 32 + c * 32 + 8 * g4;                  \
+    _Pragma("unroll") for (int db = 0; db < 8; ++db) vf[db] = KV_LD((const uint4*)(vt + db * 16 * 32));  \
+  }
+#define CH_TILE(kf, vf, kb_)                                                                       \
+  {                                                                                                \
+    _Pragma("unroll") for (int u = 0; u < QB; ++u)                                                 \
+      if ((kb_) <= bhi[u] && (kb_) + 31 >= blo[u])                                                 \
+        attn_tile(kf, vf, qf[u], (kb_), g4, cvalid[u], kbeg, kend, lo_c[u], pos_c[u], scale_log2,  \
+                  m_run[u], l_run[u], O[u]);                                                       \
+  }
+  {
+    uint4 kA[2][4], vA[8], kB[2][4], vB[8];
+    auto kb_of = [&](int i) { return t0 + 32 * min(i, ntiles - 1); };
+    CH_LOAD(kA, vA, kb_of(0));
+    int i = 0;
+    for (; i + 1 < ntiles; i += 2) {
+      CH_LOAD(kB, vB, kb_of(i + 1));
+      __builtin_amdgcn_sched_barrier(0);
+      CH_TILE(kA, vA, kb_of(i));
+      __builtin_amdgcn_sched_barrier(0);
+      CH_LOAD(kA, vA, kb_of(i + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      CH_TILE(kB, vB, kb_of(i + 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i < ntiles) CH_TILE(kA, vA, kb_of(i));
+  }
+#undef CH_TILE
+#undef CH_LOAD
+  // lane (c, g4) holds dims 16 db + 4 g4 .. +3 of column c: 8-byte stores
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    float l_tot = l_run[u] + __shfl_xor(l_run[u], 16, WAVE);
+    l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
+    if (!cvalid[u]) continue;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      uint2 pk;
+      pk.x = pack2bf(O[u][db][0] * inv, O[u][db][1] * inv);
+      pk.y = pack2bf(O[u][db][2] * inv, O[u][db][3] * inv);
+      *(uint2*)(y + frag_idx(base + j_c[u], head_c[u] * HD + 16 * db + 4 * g4, H * HD)) = pk;
+    }
+  }
+}
+
 // One workgroup per (row, KV group, query block): merge the key splits of
 // its 16 columns and normalise; thread t owns column t / 16 and 8
 // consecutive dimensions.
@@ -475,6 +589,10 @@ __global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, cons
 #ifndef FC_ATTN_TARGET_WG
 #define FC_ATTN_TARGET_WG 256
 #endif
+// query columns per row from which a chunk takes k_attn_chunk
+#ifndef FC_ATTN_CHUNK_COLS
+#define FC_ATTN_CHUNK_COLS 128
+#endif
 // waves per attention workgroup (they take the block's 32-key tiles round robin)
 #ifndef FC_ATTN_WAVES
 #define FC_ATTN_WAVES 4
@@ -517,7 +635,15 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
   FC_CHECK_ARG(cap % 32 == 0, "cache capacity must be a multiple of 32");
   FC_CHECK_ARG(max_per_row > 0, "max_per_row");
   const float scale = 1.f / sqrtf((float)hd);
-  if (dtype == FC_BF16 && hd == 128) {
+  if (dtype == FC_BF16 && hd == 128 && typ_per_row * (H / G) >= FC_ATTN_CHUNK_COLS) {
+    // prefill-width chunks: QB query blocks per wave, 4 waves per workgroup
+    constexpr int QB = 2;
+    const int nqblk = (max_per_row * (H / G) + 15) / 16;
+    FC_CHECK_ARG(B * G <= 65535, "batch * n_kv_head must be <= 65535");
+    hipLaunchKernelGGL(k_attn_chunk<QB>, dim3((nqblk + 4 * QB - 1) / (4 * QB), B * G), dim3(256), 0, s,
+                       (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, (bf16_t*)y, H, G, cap, row_off, start,
+                       max_per_row, max_tokens, window, scale * 1.4426950408889634f);
+  } else if (dtype == FC_BF16 && hd == 128) {
     AttnGrid a = fc_attn_grid(B, max_per_row, typ_per_row, H, G, max_keys);
     const int64_t units = (int64_t)B * G * a.nqblk * a.nsplit * 16;
     FC_CHECK_ARG(part != nullptr && part_bytes >= fc_align(units * 128 * 4) + fc_align(units * 2 * 4),
