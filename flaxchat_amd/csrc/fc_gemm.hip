@@ -935,7 +935,30 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
   // lane l holds row 32 p + l % 32 of the quadrant; register 4 j + x holds
   // column 32 q + 8 j + 4 (l / 32) + x
   const int rl = lane & 31, ch = 4 * (lane >> 5);
-  if constexpr (EPI == EPI_RELU2) {
+  if constexpr (EPI == EPI_QKV) {
+    // the quadrant is one head slot (128 columns) for 128 tokens: per 32
+    // tokens, stage the rows in this wave's own LDS stage (fp32), then eight
+    // lanes per token finish RoPE / QK-norm / VE gate / KV append
+    BigStage* mine = wave == 0 ? &s0 : wave == 1 ? &s1 : wave == 2 ? &s2 : &s3;
+    float(*T)[128 + 4] = (float(*)[128 + 4])mine;
+    const int hh = (n0 + 128 * wn) >> 7;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *(float4*)&T[rl][32 * q + 8 * j + ch] =
+              float4{acc[p][q][4 * j], acc[p][q][4 * j + 1], acc[p][q][4 * j + 2], acc[p][q][4 * j + 3]};
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int tt = 8 * it + (lane >> 3);
+        qkv_finish(e.qkv, T[tt], m0 + 128 * wm + 32 * p + tt, M, hh, lane & 7);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  } else if constexpr (EPI == EPI_RELU2) {
     // bf16 fragment order: per 32 x 32 block, lane l writes row l % 32,
     // columns 8 j + 4 (l / 32) .. +3 into a 32 x 80 B scratch; then per
     // 16-row half, lane L reads row L % 16, columns 8 (L / 16) .. +7
@@ -1060,6 +1083,7 @@ static void launch_big(const void* A, const void* W, int Mcap, const int* Mdev, 
     case EPI_ADD: launch_big_e<EPI_ADD>(A, W, Mcap, Mdev, N, K, e, s); break;
     case EPI_RELU2: launch_big_e<EPI_RELU2>(A, W, Mcap, Mdev, N, K, e, s); break;
     case EPI_MLPOUT: launch_big_e<EPI_MLPOUT>(A, W, Mcap, Mdev, N, K, e, s); break;
+    case EPI_QKV: launch_big_e<EPI_QKV>(A, W, Mcap, Mdev, N, K, e, s); break;
     default: launch_big_e<EPI_SOFTCAP>(A, W, Mcap, Mdev, N, K, e, s); break;
   }
 }
@@ -1146,7 +1170,8 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
 bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
   if (dtype != FC_BF16 || head_dim != 128 || N % 128 != 0 || K % 64 != 0) return false;
   const GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
-  return p.dma || (p.la && p.mb == 2 && p.nb == 2);  // the QKV tile itself is k_gemm_la's 32 x 128
+  // the QKV tile itself is k_gemm_la's 32 x 128, or a 128 x 128 quadrant of k_gemm_big
+  return p.big || p.dma || (p.la && p.mb == 2 && p.nb == 2);
 }
 
 // The EPI_ADD GEMM that writes the bf16 copy of x (attention c_proj, bf16):
@@ -1184,7 +1209,8 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
                "bf16 GEMM needs K % 64 == 0 and N % 32 == 0 (fragment-order operands)");
   if (e.mode == EPI_QKV) {
     FC_CHECK_ARG(fc_gemm_fuses_qkv(Mtyp, N, K, dtype, 128), "EPI_QKV needs the 32 x 128 bf16 tile");
-    launch_la_qkv(A, W, Mcap, Mdev, N, K, e, s);
+    if (plan_gemm(Mtyp, N, K, dtype, false).big) launch_big(A, W, Mcap, Mdev, N, K, e, s);
+    else launch_la_qkv(A, W, Mcap, Mdev, N, K, e, s);
     FC_LAUNCH_CHECK();
     return FC_OK;
   }
