@@ -786,9 +786,10 @@ __device__ __forceinline__ f32x16 mfma32(v4u a, v4u b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                   0, 0);
 }
+template <int NB>
 struct BigStage {
   uint4 a[16][64];
-  uint4 w[16][64];
+  uint4 w[4 * NB][64];
 };
 template <int EPI>
 __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0, float v1, float v2, float v3) {
@@ -823,12 +824,15 @@ __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0,
     epi_apply<EPI>(e, m, n + 3, v3);
   }
 }
-template <int EPI>
+template <int EPI, int NB>
 __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
                                                   int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
                                                   int mtiles, int per_xcd, Epi e) {
-  constexpr int NSTG = 4, GM = 4;
-  __shared__ BigStage s0, s1, s2, s3;
+  // NB 32-column blocks per wave: tile 256 x 64 NB (NB = 4: 256 x 256; NB = 3: 256 x 192)
+  constexpr int NSTG = 4, GM = 4, NT = 64 * NB;
+  static_assert(NB == 3 || NB == 4, "tile widths 192 and 256");
+  static_assert(EPI != EPI_QKV || NB == 4, "the QKV epilogue needs one head (128 columns) per wave");
+  __shared__ BigStage<NB> s0, s1, s2, s3;
   // tile of this workgroup: XCD id % 8 takes grouped tiles [x per_xcd, (x + 1) per_xcd)
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if ((int)(blockIdx.x >> 3) >= per_xcd || t >= ntiles * mtiles) return;
@@ -838,40 +842,39 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
   const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
   const int m0 = mt * 256;
   if (m0 >= M) return;
-  const int n0 = nt * 256;
+  const int n0 = nt * NT;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t KS32 = K >> 5;
   const int C = K >> 5;
   const int last_blk = (M - 1) >> 4;
-  // this wave's loads: activation row blocks 4 wave .. +3 and weight column blocks 4 wave .. +3
+  // this wave's loads: activation row blocks 4 wave .. +3 and weight column blocks NB wave .. +NB-1
   const bf16_t* ab[4];
-  const bf16_t* wb[4];
+  const bf16_t* wb[NB];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    ab[u] = A + (int64_t)min(m0 / 16 + 4 * wave + u, last_blk) * KS32 * 512 + lane * 8;
-    wb[u] = W + (int64_t)(n0 / 16 + 4 * wave + u) * KS32 * 512 + lane * 8;
-  }
+  for (int u = 0; u < 4; ++u) ab[u] = A + (int64_t)min(m0 / 16 + 4 * wave + u, last_blk) * KS32 * 512 + lane * 8;
+#pragma unroll
+  for (int u = 0; u < NB; ++u) wb[u] = W + (int64_t)(n0 / 16 + NB * wave + u) * KS32 * 512 + lane * 8;
   // this lane's 32x32x16 operand slot: 16-row block offset and lane slot (half 0; +32 for half 1)
   const int sub = (lane & 31) >> 4, slot = (lane & 15) + 16 * (lane >> 5);
-  f32x16 acc[4][4];
+  f32x16 acc[4][NB];
 #pragma unroll
   for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < NB; ++q)
 #pragma unroll
       for (int x = 0; x < 16; ++x) acc[p][q][x] = 0.f;
-  constexpr int NV = 8 * (NSTG - 2);
+  constexpr int NV = (4 + NB) * (NSTG - 2);
   static_assert(NV < 64, "vmcnt range");
 #define BIG_ISSUE(S, c_)                                                                                      \
   {                                                                                                           \
     const int c = min((c_), C - 1); /* past the end: harmless re-reads into an unread stage */                \
-    _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                                           \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u)                                                             \
       __builtin_amdgcn_global_load_lds((const void*)(ab[u] + (int64_t)c * 512),                              \
                                        (__attribute__((address_space(3))) void*)&S.a[4 * wave + u][0], 16, 0, 0); \
+    _Pragma("unroll") for (int u = 0; u < NB; ++u)                                                            \
       __builtin_amdgcn_global_load_lds((const void*)(wb[u] + (int64_t)c * 512),                              \
-                                       (__attribute__((address_space(3))) void*)&S.w[4 * wave + u][0], 16, 0, 0); \
-    }                                                                                                         \
+                                       (__attribute__((address_space(3))) void*)&S.w[NB * wave + u][0], 16, 0, 0); \
   }
 #define BIG_SYNC(NVW)                                                                                         \
   {                                                                                                           \
@@ -886,17 +889,18 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
   // fragments of one k step: [half][32-row / 32-column block]
 #define BIG_READ(S, WF, AF)                                                                                   \
   {                                                                                                           \
-    _Pragma("unroll") for (int h = 0; h < 2; ++h)                                                             \
-      _Pragma("unroll") for (int b = 0; b < 4; ++b) {                                                         \
-        WF[h][b] = __builtin_bit_cast(v4u, S.w[8 * wn + 2 * b + sub][slot + 32 * h]);                         \
+    _Pragma("unroll") for (int h = 0; h < 2; ++h) {                                                           \
+      _Pragma("unroll") for (int b = 0; b < NB; ++b)                                                          \
+        WF[h][b] = __builtin_bit_cast(v4u, S.w[2 * NB * wn + 2 * b + sub][slot + 32 * h]);                    \
+      _Pragma("unroll") for (int b = 0; b < 4; ++b)                                                           \
         AF[h][b] = __builtin_bit_cast(v4u, S.a[8 * wm + 2 * b + sub][slot + 32 * h]);                         \
-      }                                                                                                       \
+    }                                                                                                         \
   }
 #define BIG_MMA(WF, AF)                                                                                       \
   {                                                                                                           \
     _Pragma("unroll") for (int h = 0; h < 2; ++h)                                                             \
       _Pragma("unroll") for (int p = 0; p < 4; ++p)                                                           \
-        _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[p][q] = mfma32(WF[h][q], AF[h][p], acc[p][q]);      \
+        _Pragma("unroll") for (int q = 0; q < NB; ++q) acc[p][q] = mfma32(WF[h][q], AF[h][p], acc[p][q]);     \
   }
   // step i: SN = stage of chunk i + 1 (read now), SI = stage of chunk i (refilled with chunk i + 4)
 #define BIG_STEP(SI, SN, WFC, AFC, WFN, AFN, i_)                                                              \
@@ -906,7 +910,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
     BIG_ISSUE(SI, (i_) + NSTG);                                                                               \
     BIG_MMA(WFC, AFC);                                                                                        \
   }
-  v4u wf0[2][4], af0[2][4], wf1[2][4], af1[2][4];
+  v4u wf0[2][NB], af0[2][4], wf1[2][NB], af1[2][4];
   BIG_ISSUE(s0, 0);
   BIG_ISSUE(s1, 1);
   BIG_ISSUE(s2, 2);
@@ -939,7 +943,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
     // the quadrant is one head slot (128 columns) for 128 tokens: per 32
     // tokens, stage the rows in this wave's own LDS stage (fp32), then eight
     // lanes per token finish RoPE / QK-norm / VE gate / KV append
-    BigStage* mine = wave == 0 ? &s0 : wave == 1 ? &s1 : wave == 2 ? &s2 : &s3;
+    BigStage<NB>* mine = wave == 0 ? &s0 : wave == 1 ? &s1 : wave == 2 ? &s2 : &s3;
     float(*T)[128 + 4] = (float(*)[128 + 4])mine;
     const int hh = (n0 + 128 * wn) >> 7;
 #pragma unroll
@@ -968,7 +972,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < NB; ++q) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           uint32_t pk[2];
@@ -979,7 +983,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
           }
           *(uint2*)(scr + rl * 80 + (8 * j + ch) * 2) = uint2{pk[0], pk[1]};
         }
-        const int kb = (n0 + 128 * wn + 32 * q) >> 5;
+        const int kb = (n0 + 32 * NB * wn + 32 * q) >> 5;
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) {
           const uint4 val = *(const uint4*)(scr + (16 * hs + (lane & 15)) * 80 + 16 * (lane >> 4));
@@ -994,10 +998,10 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
       const int m = m0 + 128 * wm + 32 * p + rl;
       if (m < M) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < NB; ++q)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            big_store4<EPI>(e, m, n0 + 128 * wn + 32 * q + 8 * j + ch, acc[p][q][4 * j], acc[p][q][4 * j + 1],
+            big_store4<EPI>(e, m, n0 + 32 * NB * wn + 32 * q + 8 * j + ch, acc[p][q][4 * j], acc[p][q][4 * j + 1],
                             acc[p][q][4 * j + 2], acc[p][q][4 * j + 3]);
       }
     }
@@ -1068,24 +1072,34 @@ static void launch_dma(const void* A, const void* W, int Mcap, const int* Mdev, 
                                            (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, mtiles, mfast, e));
 }
 
-template <int EPI>
+template <int EPI, int NB>
 static void launch_big_e(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
                          hipStream_t s) {
-  const int ntiles = N / 256, mtiles = (Mcap + 255) / 256;
+  const int ntiles = N / (64 * NB), mtiles = (Mcap + 255) / 256;
   const int per_xcd = (ntiles * mtiles + 7) / 8;
-  hipLaunchKernelGGL((k_gemm_big<EPI>), dim3(8 * per_xcd), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W, Mcap,
-                     Mdev, N, K, ntiles, mtiles, per_xcd, e);
+  hipLaunchKernelGGL((k_gemm_big<EPI, NB>), dim3(8 * per_xcd), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W,
+                     Mcap, Mdev, N, K, ntiles, mtiles, per_xcd, e);
+}
+// 256-column tiles unless they leave CUs idle in a single partial wave of
+// workgroups and 192 divides N (n_embd-wide outputs: 1536 = 8 x 192)
+static int big_tile_blocks(int Mcap, int N) {
+  const int mtiles = (Mcap + 255) / 256;
+  if (N % 256 == 0 && (N / 256) * mtiles >= 240) return 4;
+  return N % 192 == 0 ? 3 : 4;
 }
 static void launch_big(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
                        hipStream_t s) {
+  const bool w192 = e.mode != EPI_QKV && big_tile_blocks(Mcap, N) == 3;
+#define BIG_NB(E) (w192 ? launch_big_e<E, 3>(A, W, Mcap, Mdev, N, K, e, s) : launch_big_e<E, 4>(A, W, Mcap, Mdev, N, K, e, s))
   switch (e.mode) {
-    case EPI_STORE: launch_big_e<EPI_STORE>(A, W, Mcap, Mdev, N, K, e, s); break;
-    case EPI_ADD: launch_big_e<EPI_ADD>(A, W, Mcap, Mdev, N, K, e, s); break;
-    case EPI_RELU2: launch_big_e<EPI_RELU2>(A, W, Mcap, Mdev, N, K, e, s); break;
-    case EPI_MLPOUT: launch_big_e<EPI_MLPOUT>(A, W, Mcap, Mdev, N, K, e, s); break;
-    case EPI_QKV: launch_big_e<EPI_QKV>(A, W, Mcap, Mdev, N, K, e, s); break;
-    default: launch_big_e<EPI_SOFTCAP>(A, W, Mcap, Mdev, N, K, e, s); break;
+    case EPI_STORE: BIG_NB(EPI_STORE); break;
+    case EPI_ADD: BIG_NB(EPI_ADD); break;
+    case EPI_RELU2: BIG_NB(EPI_RELU2); break;
+    case EPI_MLPOUT: BIG_NB(EPI_MLPOUT); break;
+    case EPI_QKV: launch_big_e<EPI_QKV, 4>(A, W, Mcap, Mdev, N, K, e, s); break;
+    default: BIG_NB(EPI_SOFTCAP); break;
   }
+#undef BIG_NB
 }
 
 static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
