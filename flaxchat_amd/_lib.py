@@ -39,10 +39,13 @@ class FcCache(Structure):
     _fields_ = [("k", c_void_p), ("v", c_void_p), ("hist", c_void_p), ("batch", c_int32), ("cap", c_int32)]
 
 
+FC_CHUNK_FULL_SMEAR = 1  # fc_chunk.flags: the full-sequence forward's smear
+
+
 class FcChunk(Structure):
     _fields_ = [("max_tokens", c_int32), ("max_per_row", c_int32), ("typ_tokens", c_int32),
                 ("tokens", c_void_p), ("row_off", c_void_p), ("start", c_void_p),
-                ("n_out", c_int32), ("logits", c_void_p), ("logits_stride", c_int64)]
+                ("n_out", c_int32), ("logits", c_void_p), ("logits_stride", c_int64), ("flags", c_int32)]
 
 
 class FcRowstat(Structure):
@@ -64,7 +67,7 @@ class FcSpecState(Structure):
 
 EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forward", "fc_gemm", "fc_pack_operand",
            "fc_attention_workspace_bytes", "fc_attention", "fc_row_stats", "fc_spec_workspace_bytes",
-           "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_engine_sample",
+           "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_engine_sample", "fc_cross_entropy",
            "fc_graph_begin", "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
 
 _lib = None
@@ -102,6 +105,8 @@ def _declare(L):
     L.fc_fast_sample.restype = i32
     L.fc_engine_sample.argtypes = [vp, i32, i32, f32, i32, c_uint64, vp, vp, i32, vp, vp, vp, vp, vp]
     L.fc_engine_sample.restype = i32
+    L.fc_cross_entropy.argtypes = [vp, i64, vp, i32, i32, vp, vp]
+    L.fc_cross_entropy.restype = i32
     L.fc_graph_begin.argtypes = [vp]
     L.fc_graph_begin.restype = i32
     L.fc_graph_end.argtypes = [vp, POINTER(c_void_p)]

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
                                                const int* __restrict__ start, int max_per_row, int Mcap, int D,
                                                int cap, float* __restrict__ hist, float* __restrict__ x,
                                                float* __restrict__ x0, int* __restrict__ tok_row,
-                                               int* __restrict__ tok_pos) {
+                                               int* __restrict__ tok_pos, int full_smear) {
   __shared__ float sg[EMBED_MAXW], sinv[EMBED_MAXW];
   const int b = blockIdx.x;
   const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
@@ -98,15 +98,16 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
       for (int u = 0; u < EMBED_AHEAD; ++u) {
         const int j = j0 + u;
         if (j < n) {
-          float xv[8], xr[8];
+          float xv[8], xr[8], nv[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            xv[i] = ev[u][i] * sinv[j] + sg[j] * prev[i];
+            nv[i] = ev[u][i] * sinv[j];
+            xv[i] = nv[i] + sg[j] * prev[i];
             xr[i] = r0 * xv[i] + a0 * xv[i];
-            prev[i] = xv[i];
+            prev[i] = full_smear ? nv[i] : xv[i];  // GPT.__call__ smears with n_{t-1}, decode with x_{t-1}
           }
           const int pos = s0 + j;
-          if (pos < cap) st8(hist + ((int64_t)b * cap + pos) * D + c0, xv);
+          if (pos < cap) st8(hist + ((int64_t)b * cap + pos) * D + c0, prev);
           const int64_t m = base + j;
           st8(x0 + m * D + c0, xv);
           st8(x + m * D + c0, xr);
@@ -312,15 +313,19 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   // attention c_proj keeps a bf16 copy of x and per-tile sums of squares,
   // c_fc scales its rows by 1 / rms); fp32 keeps the exact RMSNorm kernel
   const bool fold = dt == FC_BF16 && fc_gemm_fold_ok(Mtyp, D);
+  FC_CHECK_ARG((ch->flags & ~FC_CHUNK_FULL_SMEAR) == 0, "unknown fc_chunk flags");
+  const int full_smear = ch->flags & FC_CHUNK_FULL_SMEAR;
 
   if (dt == FC_BF16)
     hipLaunchKernelGGL(k_embed<bf16_t>, dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
-                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
+                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
+                       full_smear);
   else
     hipLaunchKernelGGL(k_embed<float>, dim3(B), dim3(256), 0, s, (const float*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
-                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos);
+                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
+                       full_smear);
   FC_LAUNCH_CHECK();
 
   Pending pend{};

@@ -1198,3 +1198,38 @@ extern "C" int32_t fc_engine_sample(const float* logits, int32_t batch, int32_t 
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Cross-entropy of the full-sequence forward (flaxchat/gpt.py:446-452):
+// one workgroup per logits row, max then sum of exp (fixed reduction order)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_cross_entropy(const float* __restrict__ logits, int64_t row_stride,
+                                                       const int* __restrict__ targets, int V,
+                                                       float* __restrict__ loss) {
+  __shared__ float red[16];
+  const int r = blockIdx.x;
+  const int t = targets[r];
+  if (t < 0 || t >= V) {  // masked rows (the caller keeps t < V)
+    if (threadIdx.x == 0) loss[r] = 0.f;
+    return;
+  }
+  const float* z = logits + (int64_t)r * row_stride;
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < V; i += blockDim.x) mx = fmaxf(mx, z[i]);
+  mx = block_max(mx, red);
+  float s = 0.f;
+  for (int i = threadIdx.x; i < V; i += blockDim.x) s += expf(z[i] - mx);
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) loss[r] = (mx + logf(s)) - z[t];
+}
+
+extern "C" int32_t fc_cross_entropy(const float* logits, int64_t row_stride, const int32_t* targets, int32_t rows,
+                                    int32_t V, float* loss, void* stream) {
+  FC_CHECK_ARG(logits && targets && loss, "null pointer");
+  FC_CHECK_ARG(rows >= 0 && V > 0 && row_stride >= V, "sizes");
+  if (rows == 0) return FC_OK;
+  hipLaunchKernelGGL(k_cross_entropy, dim3(rows), dim3(256), 0, (hipStream_t)stream, logits, row_stride, targets, V,
+                     loss);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}

@@ -680,6 +680,60 @@ class StreamSession:
             pass
 
 
+# ---------------------------------------------------------------------------
+# Full-sequence forward: GPT.__call__ (flaxchat/gpt.py:407-454)
+# ---------------------------------------------------------------------------
+_FULL_CHUNK = 1024  # tokens per row per forward chunk (the embed kernel's limit)
+
+
+def gpt_forward(model, idx, targets=None, *, dtype=None, device=None, chunk: int = _FULL_CHUNK):
+    """GPT.__call__(idx, targets=None) on the HIP engine (flaxchat/gpt.py:407-454).
+
+    idx: [B, T] token ids (list of lists, array or tensor). Returns the
+    softcapped fp32 logits [B, T, vocab] as a device tensor or, with
+    targets [B, T] (entries < 0 are masked), the mean cross-entropy over the
+    unmasked positions as a 0-d device tensor. The forward is the engine's
+    packed-chunk forward over all positions (chunks of up to `chunk` tokens
+    per row, each position's logits kept), with the full-sequence smear
+    (gate_t * n_{t-1}, FC_CHUNK_FULL_SMEAR) instead of the decode one."""
+    dm = as_device_model(model, dtype, device)
+    dev = dm.device
+    ids = torch.as_tensor(np.asarray(idx.cpu() if torch.is_tensor(idx) else idx), dtype=torch.int32)
+    if ids.dim() != 2 or ids.shape[1] == 0:
+        raise ValueError("idx must be [B, T] with T >= 1")
+    B, T = ids.shape
+    if int(ids.min()) < 0 or int(ids.max()) >= dm.V:
+        raise ValueError(f"token ids must be in [0, {dm.V})")
+    if T > dm.t["rope_cos"].shape[0]:
+        raise ValueError("sequence exceeds the RoPE table")
+    chunk = max(1, min(int(chunk), _FULL_CHUNK))
+    cache = DeviceCache(dm, B, T)
+    ws = Workspace(dev)
+    logits = torch.empty(B, T, dm.V, dtype=torch.float32, device=dev)
+    ids_dev = ids.to(dev)
+    for c0 in range(0, T, chunk):
+        n = min(chunk, T - c0)
+        tok = ids_dev[:, c0:c0 + n].contiguous().view(-1)
+        off = torch.arange(0, B * n + 1, n, dtype=torch.int32, device=dev)
+        start = torch.full((B,), c0, dtype=torch.int32, device=dev)
+        forward_packed(dm, cache, tok, off, start, n, n, logits[:, c0:], ws, logits_stride=T * dm.V,
+                       flags=_lib.FC_CHUNK_FULL_SMEAR)
+    if targets is None:
+        return logits
+    tgt = torch.as_tensor(np.asarray(targets.cpu() if torch.is_tensor(targets) else targets), dtype=torch.int32)
+    if tuple(tgt.shape) != (B, T):
+        raise ValueError("targets must have the shape of idx")
+    if int(tgt.max()) >= dm.V:
+        raise ValueError(f"targets must be < {dm.V} (negative entries are masked)")
+    tgt_dev = tgt.to(dev).contiguous().view(-1)
+    loss = torch.empty(B * T, dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    check(lib().fc_cross_entropy(logits.data_ptr(), dm.V, tgt_dev.data_ptr(), B * T, dm.V, loss.data_ptr(), s),
+          "fc_cross_entropy")
+    mask = (tgt_dev >= 0).float()
+    return loss.sum() / torch.clamp(mask.sum(), min=1.0)
+
+
 class Engine:
     """The reference Engine (flaxchat/engine.py:661-908): streaming
     generation with tool use, and the fast / speculative decode entry points.

@@ -111,6 +111,13 @@ class GPT:
             return self.wte.embedding.T
         return self.lm_head.kernel
 
+    def __call__(self, idx, targets=None, *, dtype=None, device=None):
+        """GPT.__call__(idx, targets=None) (flaxchat/gpt.py:407-454) on the
+        HIP engine: softcapped fp32 logits [B, T, vocab], or with targets
+        the mean cross-entropy over targets >= 0 (device tensors)."""
+        from .engine import gpt_forward
+        return gpt_forward(self, idx, targets, dtype=dtype, device=device)
+
     # ------------------------------------------------------------------
     # Initialisation recipes
     # ------------------------------------------------------------------

@@ -269,7 +269,8 @@ class Workspace:
 
 def forward_packed(dm: DeviceModel, cache: DeviceCache, tokens: torch.Tensor, row_off: torch.Tensor,
                    start: torch.Tensor, max_per_row: int, n_out: int, logits: Optional[torch.Tensor],
-                   ws: Workspace, stream=None, logits_stride: Optional[int] = None, typ_tokens: int = 0):
+                   ws: Workspace, stream=None, logits_stride: Optional[int] = None, typ_tokens: int = 0,
+                   flags: int = 0):
     """Feed a packed chunk (include/flaxchat_amd.h, fc_chunk): row b's tokens
     are tokens[row_off[b]:row_off[b+1]] at positions start[b].. (device int32
     arrays; tokens has the chunk's capacity). Writes softcapped logits of the
@@ -283,7 +284,7 @@ def forward_packed(dm: DeviceModel, cache: DeviceCache, tokens: torch.Tensor, ro
     buf = ws.get(nbytes)
     stride = logits_stride if logits_stride is not None else n_out * dm.V
     ch = FcChunk(max_tokens, max_per_row, typ_tokens, tokens.data_ptr(), row_off.data_ptr(), start.data_ptr(),
-                 n_out, _ptr(logits) if n_out > 0 else 0, stride)
+                 n_out, _ptr(logits) if n_out > 0 else 0, stride, flags)
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
     check(lib().fc_forward(ctypes.byref(dm.desc), ctypes.byref(cache.desc), ctypes.byref(ch),
                            buf.data_ptr(), buf.numel(), s), "fc_forward")

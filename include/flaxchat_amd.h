@@ -102,7 +102,15 @@ typedef struct fc_chunk {
   float* logits;          /* row (b, r) at logits + b*logits_stride + r*V;    */
                           /* unspecified for a row with fewer than n_out tokens */
   int64_t logits_stride;  /* floats between rows b and b+1                    */
+  int32_t flags;          /* FC_CHUNK_* bits; 0 = the per-token decode forward  */
 } fc_chunk;
+
+/* fc_chunk.flags: smear as the full-sequence forward GPT.__call__ does
+ * (flaxchat/gpt.py:418-421): x_t = n_t + gate_t * n_{t-1} with n the
+ * normalised embeddings, where the per-token decode forward
+ * (flaxchat/engine.py:84-87) adds gate_t * x_{t-1}, the previous smeared
+ * value. The cache's smear history then holds n for the next chunk. */
+#define FC_CHUNK_FULL_SMEAR 1
 
 /* Per-row sampling statistics of a logits row (see fc_row_stats). */
 typedef struct fc_rowstat {
@@ -253,6 +261,13 @@ int32_t fc_engine_sample(const float* logits, int32_t batch, int32_t V, float te
                          int32_t top_k, uint64_t seed, const int32_t* forced, int32_t* gen,
                          int32_t gen_cap, int32_t* pos, int32_t* step, int32_t* tok_cur,
                          fc_rowstat* stats, void* stream);
+
+/* Cross-entropy of GPT.__call__(idx, targets) (flaxchat/gpt.py:446-452):
+ * for each of `rows` logits rows (row r at logits + r * row_stride, V
+ * entries), loss[r] = logsumexp(z) - z[target[r]] in fp32, or 0 when
+ * target[r] < 0 (masked); target[r] >= V is an error the caller excludes. */
+int32_t fc_cross_entropy(const float* logits, int64_t row_stride, const int32_t* targets, int32_t rows,
+                         int32_t V, float* loss, void* stream);
 
 /* Stream capture into a replayable hipGraph (the captured draft loop). */
 int32_t fc_graph_begin(void* stream);

@@ -1,0 +1,91 @@
+"""GPT.__call__ on the HIP engine (flaxchat_amd.engine.gpt_forward) against
+the oracle's full-sequence forward (oracle/full.py). Tolerances as the rest
+of the suite: fp32 logits within 1e-3 max-abs,
+bf16 within 5e-2; the loss within 1e-4 relative in fp32."""
+
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from flaxchat_amd.engine import gpt_forward  # noqa: E402
+from oracle.full import gpt_call  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("which", ["tiny", "cfg1"])
+def test_full_forward_fp32(which, tiny_pair, cfg1_pair):
+    _say(f"full forward fp32 {which}")
+    m = (tiny_pair if which == "tiny" else cfg1_pair)[0]
+    ids = np.random.default_rng(7).integers(0, m.config.vocab_size, (3, 37))
+    got = gpt_forward(m, ids, dtype="fp32").cpu().numpy()
+    ref = gpt_call(m, ids)
+    assert got.shape == ref.shape
+    assert np.abs(got - ref).max() < 1e-3
+
+
+def test_full_forward_smear_is_the_full_sequence_one(tiny_pair):
+    """tiny_pair's target has a non-zero smear: the device result follows
+    GPT.__call__, not the decode recurrence."""
+    from oracle.model import OracleModel
+    m = tiny_pair[0]
+    ids = np.random.default_rng(8).integers(0, m.config.vocab_size, (1, 12))
+    got = gpt_forward(m, ids, dtype="fp32").cpu().numpy()[0]
+    om = OracleModel(m)
+    st = om.new_state(16)
+    dec = np.stack([om.step(int(t), i, st) for i, t in enumerate(ids[0])])
+    assert np.abs(got - gpt_call(m, ids)[0]).max() < 1e-3
+    assert np.abs(got[2:] - dec[2:]).max() > 1e-2
+
+
+def test_full_forward_chunks(tiny_pair):
+    """Several chunks per row (the smear history carries n_{t-1} across a
+    chunk boundary) equal one chunk."""
+    _say("full forward chunked")
+    m = tiny_pair[0]
+    ids = np.random.default_rng(9).integers(0, m.config.vocab_size, (2, 45))
+    one = gpt_forward(m, ids, dtype="fp32").cpu().numpy()
+    many = gpt_forward(m, ids, dtype="fp32", chunk=16).cpu().numpy()
+    assert np.abs(one - many).max() < 1e-5
+
+
+def test_full_forward_bf16_prefill_kernels(cfg1_pair):
+    """bf16 at > 1024 tokens per chunk (256 x 256 GEMM tiles, chunk attention)."""
+    _say("full forward bf16 cfg1 4 x 300")
+    m = cfg1_pair[0]
+    ids = np.random.default_rng(10).integers(0, m.config.vocab_size, (4, 300))
+    got = gpt_forward(m, ids, dtype="bf16").cpu().numpy()
+    ref = gpt_call(m, ids)
+    assert np.abs(got - ref).max() < 5e-2
+
+
+def test_full_forward_loss(tiny_pair):
+    _say("full forward loss")
+    m = tiny_pair[0]
+    rng = np.random.default_rng(11)
+    ids = rng.integers(0, m.config.vocab_size, (3, 20))
+    tg = rng.integers(0, m.config.vocab_size, (3, 20))
+    tg[0, :4] = -1
+    tg[2, -6:] = -1
+    got = float(gpt_forward(m, ids, tg, dtype="fp32"))
+    ref = gpt_call(m, ids, tg)
+    assert abs(got - ref) < 1e-4 * max(1.0, abs(ref))
+    assert float(gpt_forward(m, ids, np.full((3, 20), -1), dtype="fp32")) == 0.0
+    # the container's __call__ is the same entry point
+    assert abs(float(m(ids, tg, dtype="fp32")) - got) < 1e-6
+
+
+def test_full_forward_rejects_bad_input(tiny_pair):
+    m = tiny_pair[0]
+    with pytest.raises(ValueError):
+        gpt_forward(m, [[1, 2, m.config.vocab_size]], dtype="fp32")
+    with pytest.raises(ValueError):
+        gpt_forward(m, [[1, 2, 3]], [[1, 2]], dtype="fp32")
