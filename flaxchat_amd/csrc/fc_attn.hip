@@ -363,6 +363,165 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
   }
 }
 
+// The same for QB query blocks per workgroup (GQA verify chunks: tokens x
+// heads-per-group > 16 columns): each wave applies every K/V tile it loads
+// to all QB blocks, so the key range is read once per QB blocks instead of
+// once per block; the waves are merged block by block. grid (key split,
+// row x KV group, group of QB query blocks).
+template <int NW, int QB>
+__global__ __launch_bounds__(64 * NW) void k_attn_mfma_qb(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+                                                       const bf16_t* __restrict__ vc, float* __restrict__ part_o,
+                                                       float* __restrict__ part_ml, bf16_t* __restrict__ y, int H,
+                                                       int G, int cap, const int* __restrict__ row_off,
+                                                       const int* __restrict__ start, int max_per_row, int Mcap,
+                                                       int window, int split_keys, int nsplit, int nqblk,
+                                                       float scale_log2) {
+  constexpr int HD = 128;
+  const int split = blockIdx.x, bg = blockIdx.y, qb0 = blockIdx.z * QB;
+  const int b = bg / G, g = bg - b * G, rep = H / G;
+  const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
+  const int base = sp.base, n = sp.n, s0 = start[b];
+  const int ncol = n * rep;
+  if (qb0 * 16 >= ncol) return;  // no query of this row in the group: combine reads nothing here
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, g4 = lane >> 4;
+  const int nblk = min(QB, (ncol - qb0 * 16 + 15) / 16);  // blocks of the group holding a query
+
+  // key range of the whole group of query blocks
+  const int f = qb0 * 16, lcol = min(qb0 * 16 + 16 * QB - 1, ncol - 1);
+  int kbeg = 0, kend = 0;
+  {
+    const int pf = s0 + f / rep, pl = s0 + lcol / rep;
+    const int klo = window > 0 ? max(0, pf - window) : 0;
+    const int khi = min(pl + 1, cap);
+    kbeg = klo + split * split_keys;
+    kend = min(khi, kbeg + split_keys);
+  }
+  if (kbeg >= kend) {  // only with several splits: a query always sees itself
+    if (threadIdx.x < 16) {
+      for (int u = 0; u < nblk; ++u) {
+        const int64_t pidx = ((int64_t)bg * nqblk + qb0 + u) * nsplit + split;
+        part_ml[(pidx * 16 + threadIdx.x) * 2 + 0] = -INFINITY;
+        part_ml[(pidx * 16 + threadIdx.x) * 2 + 1] = 0.f;
+      }
+    }
+    return;
+  }
+  // this lane's query column in each block
+  bool cvalid[QB];
+  int pos_c[QB], lo_c[QB];
+  uint4 qf[QB][4];
+  const uint4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    const int col = (qb0 + u) * 16 + c;
+    const int j = col / rep, head = g * rep + (col - j * rep);
+    cvalid[u] = col < ncol;
+    pos_c[u] = s0 + j;
+    lo_c[u] = window > 0 ? max(0, pos_c[u] - window) : 0;
+    const bf16_t* qr = q + ((int64_t)(base + (cvalid[u] ? j : 0)) * H + (cvalid[u] ? head : 0)) * HD + 8 * g4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[u][s] = cvalid[u] ? *(const uint4*)(qr + 32 * s) : zero;
+  }
+  const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
+  const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
+  const int r = c;
+
+  float m_run[QB], l_run[QB];
+  f32x4 O[QB][8];
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    m_run[u] = -INFINITY;
+    l_run[u] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) O[u][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // K blocks of 32 keys in fragment order: load (cc, s) of a tile is 1 KB
+  // contiguous; V blocks are [128 dims][32 keys], one 1 KB load per db
+  const int t0 = kbeg & ~31;
+  const int ntiles = (kend - t0 + 31) >> 5;
+  for (int t = wave; t < ntiles; t += NW) {
+    const int kb = t0 + 32 * t;
+    uint4 kf[2][4], vf[8];
+    const bf16_t* kt = kbase + (int64_t)(kb >> 5) * 32 * HD + lane * 8;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[cc][s] = KV_LD((const uint4*)(kt + (s * 2 + cc) * 512));
+    const bf16_t* vt = vbase + (int64_t)(kb >> 5) * HD * 32 + r * 32 + 8 * g4;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) vf[db] = KV_LD((const uint4*)(vt + db * 16 * 32));
+#pragma unroll
+    for (int u = 0; u < QB; ++u)
+      if (u < nblk)
+        attn_tile(kf, vf, qf[u], kb, g4, cvalid[u], kbeg, kend, lo_c[u], pos_c[u], scale_log2, m_run[u], l_run[u],
+                  O[u]);
+  }
+  // merge the NW waves in LDS, block by block; thread t < 256 then owns
+  // column t / 16 and dims 8 (t % 16) .. +7. A single key split writes y
+  // directly (normalised, in the c_proj operand layout); otherwise the
+  // unnormalised partial and its (max, sum) go to k_attn_combine.
+  __shared__ float sm[NW][16], sl[NW][16];
+  __shared__ float so[NW][16][HD + 4];
+#pragma unroll
+  for (int u = 0; u < QB; ++u) {
+    if (u >= nblk) break;  // uniform over the workgroup
+    const int qb = qb0 + u;
+    const int64_t pidx = ((int64_t)bg * nqblk + qb) * nsplit + split;
+    float l_tot = l_run[u] + __shfl_xor(l_run[u], 16, WAVE);
+    l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
+    if (u > 0) __syncthreads();  // the previous block's readers are done with the LDS
+    if (g4 == 0) {
+      sm[wave][c] = m_run[u];
+      sl[wave][c] = l_tot;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) so[wave][c][16 * db + 4 * g4 + i] = O[u][db][i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int qc = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w][qc]);
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      float L = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float a = exp2f(sm[w][qc] - M);
+          L += a * sl[w][qc];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] += a * so[w][qc][d0 + i];
+        }
+      }
+      const int colq = qb * 16 + qc;
+      if (nsplit == 1) {
+        if (colq < ncol) {
+          const int jq = colq / rep, hq = g * rep + (colq - jq * rep);
+          const float inv = L > 0.f ? 1.f / L : 0.f;
+          uint4 pk;
+          pk.x = pack2bf(o[0] * inv, o[1] * inv);
+          pk.y = pack2bf(o[2] * inv, o[3] * inv);
+          pk.z = pack2bf(o[4] * inv, o[5] * inv);
+          pk.w = pack2bf(o[6] * inv, o[7] * inv);
+          *(uint4*)(y + frag_idx(base + jq, hq * HD + d0, H * HD)) = pk;
+        }
+      } else {
+        float4* po = (float4*)(part_o + (pidx * 16 + qc) * HD + d0);
+        po[0] = make_float4(o[0], o[1], o[2], o[3]);
+        po[1] = make_float4(o[4], o[5], o[6], o[7]);
+        if (d0 == 0) {
+          part_ml[(pidx * 16 + qc) * 2 + 0] = M;
+          part_ml[(pidx * 16 + qc) * 2 + 1] = L;
+        }
+      }
+    }
+  }
+}
+
 // Prefill-width chunks (many queries per row): each wave owns QB query
 // blocks of 16 columns of one (row, KV group) and walks every 32-key tile of
 // their combined key range itself, so each K/V tile is read once per QB
@@ -605,7 +764,9 @@ AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, i
   // split the key range so that the blocks a typical chunk fills reach ~4
   // workgroups per CU
   const int typ_blk = std::min(a.nqblk, std::max(1, (typ_per_row * rep + 15) / 16));
-  const int64_t units = (int64_t)batch * n_kv_head * typ_blk;
+  // two query blocks per workgroup when a typical row x group fills more than one
+  a.qb = typ_blk >= 2 ? 2 : 1;
+  const int64_t units = (int64_t)batch * n_kv_head * ((typ_blk + a.qb - 1) / a.qb);
   const int range = max(max_keys, 1);
   int want = (int)((FC_ATTN_TARGET_WG + units - 1) / units);
   want = max(1, min(want, (range + 127) / 128));
@@ -651,10 +812,16 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
     float* po = (float*)part;
     float* pml = (float*)((char*)part + fc_align(units * 128 * 4));
     FC_CHECK_ARG(B * G <= 65535, "batch * n_kv_head must be <= 65535");
-    hipLaunchKernelGGL(k_attn_mfma<FC_ATTN_WAVES>, dim3(a.nsplit, B * G, a.nqblk), dim3(64 * FC_ATTN_WAVES), 0, s,
-                       (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, po, pml, (bf16_t*)y, H, G, cap, row_off,
-                       start, max_per_row, max_tokens, window, a.split_keys, a.nsplit, a.nqblk,
-                       scale * 1.4426950408889634f);
+    const float sl2 = scale * 1.4426950408889634f;
+    if (a.qb == 2)
+      hipLaunchKernelGGL((k_attn_mfma_qb<FC_ATTN_WAVES, 2>), dim3(a.nsplit, B * G, (a.nqblk + 1) / 2),
+                         dim3(64 * FC_ATTN_WAVES), 0, s, (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, po,
+                         pml, (bf16_t*)y, H, G, cap, row_off, start, max_per_row, max_tokens, window, a.split_keys,
+                         a.nsplit, a.nqblk, sl2);
+    else
+      hipLaunchKernelGGL(k_attn_mfma<FC_ATTN_WAVES>, dim3(a.nsplit, B * G, a.nqblk), dim3(64 * FC_ATTN_WAVES),
+                         0, s, (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, po, pml, (bf16_t*)y, H, G, cap,
+                         row_off, start, max_per_row, max_tokens, window, a.split_keys, a.nsplit, a.nqblk, sl2);
     if (a.nsplit > 1) {
       FC_LAUNCH_CHECK();
       hipLaunchKernelGGL(k_attn_combine<bf16_t>, dim3(B * G, a.nqblk), dim3(256), 0, s, po, pml, (bf16_t*)y, H, G,

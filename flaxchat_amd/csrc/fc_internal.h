@@ -73,6 +73,7 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
 
 struct AttnGrid {
   int nqblk, nsplit, split_keys;
+  int qb;  // query blocks per workgroup (1 or 2)
 };
 AttnGrid fc_attn_grid(int batch, int max_per_row, int typ_per_row, int n_head, int n_kv_head, int max_keys);
 int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head, int head_dim, int max_keys);

@@ -165,6 +165,7 @@ def _to_kblocked(K):
     (3, 3, 4, 2, 0, 70),        # ragged, short rows
     (32, 2, 8, 8, 0, 300),      # >= 256 row x group units: one key split, output written directly
     (32, 3, 16, 8, 100, 300),   # the same with GQA 2:1 and a window
+    (1, 12, 12, 4, 0, 1500),    # GQA 3:1, 36 columns: two query blocks per workgroup with key splits
     (2, 160, 2, 2, 0, 600),     # prefill-width chunk (>= 128 columns per row): per-wave query blocks
     (3, 130, 12, 4, 300, 900),  # the same, GQA 3:1 (390 columns) and a window
     (2, 256, 4, 4, 64, 700),    # short window: blocks skip the tiles they cannot see
