@@ -790,6 +790,9 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
 #ifndef FC_BIG_M
 #define FC_BIG_M 1024
 #endif
+#ifndef FC_BIG_MIN_TILES
+#define FC_BIG_MIN_TILES 224
+#endif
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ f32x16 mfma32(v4u a, v4u b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
@@ -825,6 +828,19 @@ __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0,
     } else {                                                           // engine.py:94
       const float4 x0 = *(const float4*)(e.x0 + i);
       *xp = float4{e.r * t.x + e.a * x0.x, e.r * t.y + e.a * x0.y, e.r * t.z + e.a * x0.z, e.r * t.w + e.a * x0.w};
+    }
+  } else if constexpr (EPI == EPI_SOFTCAP) {  // logits row (m / n_out, m % n_out), columns past V dropped
+    const int b = m / e.n_out, rr = m - b * e.n_out;
+    float* o = (float*)e.out + (int64_t)b * e.row_stride + (int64_t)rr * e.V + n;
+    const float t0 = 15.f * tanhf(v0 / 15.f), t1 = 15.f * tanhf(v1 / 15.f);
+    const float t2 = 15.f * tanhf(v2 / 15.f), t3 = 15.f * tanhf(v3 / 15.f);
+    if (n + 3 < e.V && (((uintptr_t)o) & 15) == 0) {
+      *(float4*)o = float4{t0, t1, t2, t3};
+    } else {
+      if (n < e.V) o[0] = t0;
+      if (n + 1 < e.V) o[1] = t1;
+      if (n + 2 < e.V) o[2] = t2;
+      if (n + 3 < e.V) o[3] = t3;
     }
   } else {
     epi_apply<EPI>(e, m, n, v0);
@@ -1138,9 +1154,16 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     p.gemv = true;
     return p;
   }
-  if (Mtyp >= FC_BIG_M && N % 256 == 0 && K % 128 == 0) {  // prefill chunks: 256 x 256 tiles, MFMA-bound
-    p.big = true;
-    return p;
+  if (Mtyp >= FC_BIG_M && N % 256 == 0 && K % 128 == 0) {
+    // prefill chunks: 256 x 256 (or 256 x 192) tiles, MFMA-bound, when there
+    // are enough of them to occupy the CUs (verify-size M of ~1200 rows gives
+    // 5 M tiles: the 64-row kernels are faster there)
+    const int mt = (Mtyp + 255) / 256;
+    const int tiles = std::max(mt * (N / 256), N % 192 == 0 ? mt * (N / 192) : 0);
+    if (tiles >= FC_BIG_MIN_TILES) {
+      p.big = true;
+      return p;
+    }
   }
   const int C = K / 64;
   const int s_max = std::max(1, std::min(C / 4, FC_MAX_SPLIT));  // >= 1 chunk per wave

@@ -67,6 +67,21 @@ def test_full_forward_bf16_prefill_kernels(cfg1_pair):
     assert np.abs(got - ref).max() < 5e-2
 
 
+def test_full_forward_bf16_big_tiles():
+    """n_embd 1024 at 4 x 900 tokens: the QKV (fused prologue) and c_fc
+    GEMMs take the 256-row tiles, Wo / MLP c_proj the 64-row kernels."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    _say("full forward bf16 d1024 4 x 900")
+    cfg = GPTConfig(sequence_len=1024, vocab_size=1024, n_layer=2, n_head=8, n_kv_head=8, n_embd=1024,
+                    window_pattern="SL", short_window=256)
+    m = GPT.init_normal(cfg, seed=12, std=0.02).perturb_scalars()
+    ids = np.random.default_rng(12).integers(0, cfg.vocab_size, (4, 900))
+    got = gpt_forward(m, ids, dtype="bf16").cpu().numpy()
+    ref = gpt_call(m, ids)
+    assert np.abs(got - ref).max() < 5e-2
+
+
 def test_full_forward_loss(tiny_pair):
     _say("full forward loss")
     m = tiny_pair[0]

@@ -52,13 +52,17 @@ def _gemm_cases():
                     if big and (epi in (1, 4) or (dtype == "fp32" and M > 64)):
                         continue
                     cases.append((dtype, M, epi, NK))
-    # prefill-size row counts (the 256 x 256 tile kernel): ragged M, every epilogue
+    # row counts >= 1024 with few output tiles (the 64-row kernels)
     for NK in [(512, 256), (768, 1536)]:
         for M in [1024, 1100, 2304]:
             for epi in [0, 1, 2, 4]:
                 if NK[1] > 256 and M != 1100:
                     continue
                 cases.append(("bf16", M, epi, NK))
+    # prefill-size GEMMs with >= 224 tiles (the 256 x 256 / 256 x 192 tile kernel)
+    for M, NK, epis in [(3000, (4608, 256), [0, 1, 2]), (4100, (4096, 128), [0, 2, 4])]:
+        for epi in epis:
+            cases.append(("bf16", M, epi, NK))
     return cases
 
 
