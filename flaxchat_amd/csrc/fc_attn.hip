@@ -29,9 +29,6 @@
 #include "fc_common.h"
 #include "fc_internal.h"
 
-#ifndef FC_ATTN_PIPE
-#define FC_ATTN_PIPE 0
-#endif
 // K/V cache loads are streamed once per call: non-temporal loads keep them
 // from displacing reusable lines in the caches (measured ~8% faster at cfg4)
 #ifndef FC_ATTN_NT
@@ -278,35 +275,12 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
     const bf16_t* vt = vbase + (int64_t)((kb_) >> 5) * HD * 32 + r * 32 + 8 * g4;                  \
     _Pragma("unroll") for (int db = 0; db < 8; ++db) vf[db] = KV_LD((const uint4*)(vt + db * 16 * 32));  \
   }
-#if FC_ATTN_PIPE
-  // two tiles in flight per wave: the next tile's loads are issued before the
-  // current one computes (a clamped index re-reads the last tile)
-  const int nmine = ntiles > wave ? (ntiles - wave + NW - 1) / NW : 0;
-  if (nmine > 0) {
-    uint4 kA[2][4], vA[8], kB[2][4], vB[8];
-    auto kb_of = [&](int i) { return t0 + 32 * (wave + NW * min(i, nmine - 1)); };
-    ATT_LOAD(kA, vA, kb_of(0));
-    int i = 0;
-    for (; i + 1 < nmine; i += 2) {
-      ATT_LOAD(kB, vB, kb_of(i + 1));
-      __builtin_amdgcn_sched_barrier(0);
-      attn_tile(kA, vA, qf, kb_of(i), g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
-      __builtin_amdgcn_sched_barrier(0);
-      ATT_LOAD(kA, vA, kb_of(i + 2));
-      __builtin_amdgcn_sched_barrier(0);
-      attn_tile(kB, vB, qf, kb_of(i + 1), g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (i < nmine) attn_tile(kA, vA, qf, kb_of(i), g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
-  }
-#else
   for (int t = wave; t < ntiles; t += NW) {
     const int kb = t0 + 32 * t;
     uint4 kf[2][4], vf[8];
     ATT_LOAD(kf, vf, kb);
     attn_tile(kf, vf, qf, kb, g4, cvalid, kbeg, kend, lo_c, pos_c, scale_log2, m_run, l_run, O);
   }
-#endif
 #undef ATT_LOAD
   // merge the NW waves in LDS; thread t < 256 then owns column t / 16 and
   // dims 8 (t % 16) .. +7. A single key split writes y directly (normalised,

@@ -170,15 +170,8 @@ __global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* 
 // 32-wide k step; the f32x4 result holds rows 4*(l/16)+i of column l % 16.
 // ---------------------------------------------------------------------------
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-// weight fragment loads (non-temporal when FC_GEMM_W_NT)
-#ifndef FC_GEMM_W_NT
-#define FC_GEMM_W_NT 0
-#endif
-#if FC_GEMM_W_NT
-#define W_LD(p) __builtin_nontemporal_load(p)
-#else
+// weight fragment loads: plain (they are re-read across M tiles through L2)
 #define W_LD(p) (*(p))
-#endif
 // lm_head weights (the softcap epilogue) always stream non-temporally: the
 // matrix (201 MB at cfg4) is about the size of the 256 MB Infinity Cache,
 // and both the verify and the draft lm_head reading it non-temporally made
