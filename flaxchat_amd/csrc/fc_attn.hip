@@ -22,8 +22,8 @@
 //                  read from the 32-key blocked-transposed V cache as one
 //                  16-byte load per lane).
 // The four waves merge in LDS; splits merge in k_attn_combine.
-// Prefill-width chunks (>= 128 query columns per row) take k_attn_chunk:
-// each wave owns 2 query blocks and reads every K/V tile once for both.
+// Prefill-width chunks (>= 128 query columns per row) take k_attn_pf: 128
+// columns per workgroup on the 32x32x16 MFMA, K/V tiles shared through LDS.
 // fp32 path (parity mode, or head_dim != 128): one workgroup per query with
 // the reference's operation order (scores, max, exp, normalise, weighted sum).
 #include "fc_common.h"
@@ -496,116 +496,189 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma_qb(const bf16_t* __restri
   }
 }
 
-// Prefill-width chunks (many queries per row): each wave owns QB query
-// blocks of 16 columns of one (row, KV group) and walks every 32-key tile of
-// their combined key range itself, so each K/V tile is read once per QB
-// blocks (the decode kernel reads it once per block) and applied to all of
-// them from registers; no merge between waves. Two tiles are in flight per
-// wave. A block skips the tiles it cannot see (past its last position or
-// before its window). Output: normalised, in the c_proj operand layout.
-template <int QB>
-__global__ __launch_bounds__(256) void k_attn_chunk(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
-                                                    const bf16_t* __restrict__ vc, bf16_t* __restrict__ y, int H,
-                                                    int G, int cap, const int* __restrict__ row_off,
-                                                    const int* __restrict__ start, int max_per_row, int Mcap,
-                                                    int window, float scale_log2) {
+// Prefill attention on the 32x32x16 MFMA. A workgroup owns 128 query
+// columns of one (row, KV group), 32 per wave. The 32-key K / V tiles of the
+// group's key range go through a 3-stage LDS ring by direct loads (each wave
+// 4 of a tile's 16 blocks of 1 KB), so a tile is read once per 128 columns.
+// Per tile a wave computes S^T = K Q^T (32 keys x its 32 columns; lane l
+// holds column l % 32 and 16 of the keys), the online softmax in registers
+// (one swap with lane l ^ 32 per max), then O^T += V^T P^T (4 x 32 dims); the
+// P operand of a 16-key half takes 4 keys from the lane and 4 from lane
+// l ^ 32. Both K and V are read from LDS in their cache layouts with
+// lane-dependent addresses. Waves skip the tiles outside their own key range
+// but take part in every load and barrier.
+struct PfStage {
+  uint4 k[8][64];  // one 32-key block of the K cache (8 KB)
+  uint4 v[512];    // one 32-key block of the V cache: [128 dims][32 keys] (8 KB)
+};
+__global__ __launch_bounds__(256, 2) void k_attn_pf(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+                                                 const bf16_t* __restrict__ vc, bf16_t* __restrict__ y, int H, int G,
+                                                 int cap, const int* __restrict__ row_off,
+                                                 const int* __restrict__ start, int max_per_row, int Mcap,
+                                                 int window, float scale_log2) {
   constexpr int HD = 128;
+  __shared__ PfStage st0, st1, st2;
   const int bg = blockIdx.y, b = bg / G, g = bg - b * G, rep = H / G;
   const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
   const int base = sp.base, n = sp.n, s0 = start[b];
   const int ncol = n * rep;
+  const int c0 = blockIdx.x * 128;
+  if (c0 >= ncol) return;  // the whole workgroup
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int qb0 = (blockIdx.x * 4 + wave) * QB;
-  if (qb0 * 16 >= ncol) return;  // waves work independently: no barrier below
-  const int c = lane & 15, g4 = lane >> 4;
-  // this wave's key range: from the first column's window start to the last column's position
-  const int f = qb0 * 16, lcol = min(qb0 * 16 + QB * 16 - 1, ncol - 1);
-  const int pf = s0 + f / rep, pl = s0 + lcol / rep;
-  const int kbeg = window > 0 ? max(0, pf - window) : 0;
-  const int kend = min(pl + 1, cap);
-  // per block: this lane's column, its position and window start; the block's key span
-  bool cvalid[QB];
-  int pos_c[QB], lo_c[QB], head_c[QB], j_c[QB], bhi[QB], blo[QB];
-  uint4 qf[QB][4];
-  const uint4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int u = 0; u < QB; ++u) {
-    const int col = (qb0 + u) * 16 + c;
-    cvalid[u] = col < ncol;
-    const int j = cvalid[u] ? col / rep : 0;
-    j_c[u] = j;
-    head_c[u] = g * rep + (col - (col / rep) * rep);
-    pos_c[u] = s0 + j;
-    lo_c[u] = window > 0 ? max(0, pos_c[u] - window) : 0;
-    const int bl = min((qb0 + u) * 16 + 15, ncol - 1), bf = min((qb0 + u) * 16, ncol - 1);
-    bhi[u] = s0 + bl / rep;  // last position any column of the block sees
-    blo[u] = window > 0 ? max(0, s0 + bf / rep - window) : 0;
-    const bf16_t* qr = q + ((int64_t)(base + j) * H + (cvalid[u] ? head_c[u] : 0)) * HD + 8 * g4;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[u][s] = cvalid[u] ? *(const uint4*)(qr + 32 * s) : zero;
-  }
-  const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
-  const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
-  float m_run[QB], l_run[QB];
-  f32x4 O[QB][8];
-#pragma unroll
-  for (int u = 0; u < QB; ++u) {
-    m_run[u] = -INFINITY;
-    l_run[u] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) O[u][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  const int hl = lane >> 5;
+  // the workgroup's key range
+  const int lcol = min(c0 + 127, ncol - 1);
+  const int kbeg = window > 0 ? max(0, s0 + c0 / rep - window) : 0;
+  const int kend = min(s0 + lcol / rep + 1, cap);
   const int t0 = kbeg & ~31;
   const int ntiles = (kend - t0 + 31) >> 5;
-#define CH_LOAD(kf, vf, kb_)                                                                       \
-  {                                                                                                \
-    const bf16_t* kt = kbase + (int64_t)((kb_) >> 5) * 32 * HD + lane * 8;                         \
-    _Pragma("unroll") for (int cc = 0; cc < 2; ++cc)                                               \
-      _Pragma("unroll") for (int s = 0; s < 4; ++s) kf[cc][s] = KV_LD((const uint4*)(kt + (s * 2 + cc) * 512)); \
-    const bf16_t* vt = vbase + (int64_t)((kb_) >> 5) * HD * 32 + c * 32 + 8 * g4;                  \
-    _Pragma("unroll") for (int db = 0; db < 8; ++db) vf[db] = KV_LD((const uint4*)(vt + db * 16 * 32));  \
-  }
-#define CH_TILE(kf, vf, kb_)                                                                       \
-  {                                                                                                \
-    _Pragma("unroll") for (int u = 0; u < QB; ++u)                                                 \
-      if ((kb_) <= bhi[u] && (kb_) + 31 >= blo[u])                                                 \
-        attn_tile(kf, vf, qf[u], (kb_), g4, cvalid[u], kbeg, kend, lo_c[u], pos_c[u], scale_log2,  \
-                  m_run[u], l_run[u], O[u]);                                                       \
-  }
+  // this wave's columns and key range
+  const int wc0 = c0 + 32 * wave;
+  const bool wact = wc0 < ncol;
+  const int w_hi = wact ? s0 + min(wc0 + 31, ncol - 1) / rep : -1;
+  const int w_lo = window > 0 ? max(0, s0 + wc0 / rep - window) : 0;
+  // tiles inside [w_full_lo, w_full_hi] are visible to every column of the wave (no masks)
+  const bool wfull = wc0 + 31 < ncol;
+  const int w_full_hi = s0 + wc0 / rep;  // the first column's position
+  const int w_full_lo = window > 0 ? max(0, s0 + (wc0 + 31) / rep - window) : 0;
+  // this lane's column (query)
+  const int col = wc0 + (lane & 31);
+  const bool cvalid = col < ncol;
+  const int j = cvalid ? col / rep : 0;
+  const int head = g * rep + (cvalid ? col - (col / rep) * rep : 0);
+  const int pos_c = s0 + j;
+  const int lo_c = window > 0 ? max(0, pos_c - window) : 0;
+  v4u qf[8];  // dims 16 h + 8 hl .. +7 of this lane's query
   {
-    uint4 kA[2][4], vA[8], kB[2][4], vB[8];
-    auto kb_of = [&](int i) { return t0 + 32 * min(i, ntiles - 1); };
-    CH_LOAD(kA, vA, kb_of(0));
-    int i = 0;
-    for (; i + 1 < ntiles; i += 2) {
-      CH_LOAD(kB, vB, kb_of(i + 1));
-      __builtin_amdgcn_sched_barrier(0);
-      CH_TILE(kA, vA, kb_of(i));
-      __builtin_amdgcn_sched_barrier(0);
-      CH_LOAD(kA, vA, kb_of(i + 2));
-      __builtin_amdgcn_sched_barrier(0);
-      CH_TILE(kB, vB, kb_of(i + 1));
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (i < ntiles) CH_TILE(kA, vA, kb_of(i));
+    const bf16_t* qr = q + ((int64_t)(base + j) * H + head) * HD + 8 * hl;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) qf[h] = cvalid ? *(const v4u*)(qr + 16 * h) : v4u{0u, 0u, 0u, 0u};
   }
-#undef CH_TILE
-#undef CH_LOAD
-  // lane (c, g4) holds dims 16 db + 4 g4 .. +3 of column c: 8-byte stores
+  // LDS slots this lane reads: K (block, slot) per 16-dim slice h; V uint4 index per (dims block, key half)
+  const int kk = lane & 31;
+  const int kcc = (kk >> 2) & 1, kr = ((kk >> 3) << 2) | (kk & 3);
+  const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
+  const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
+  f32x16 O[4];
 #pragma unroll
-  for (int u = 0; u < QB; ++u) {
-    float l_tot = l_run[u] + __shfl_xor(l_run[u], 16, WAVE);
-    l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
-    if (!cvalid[u]) continue;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  for (int dd = 0; dd < 4; ++dd)
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
+    for (int x = 0; x < 16; ++x) O[dd][x] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+#define PF_ISSUE(S, t_)                                                                                    \
+  {                                                                                                        \
+    const int kb_ = t0 + 32 * min((t_), ntiles - 1); /* past the end: harmless re-reads */                 \
+    const bf16_t* kt = kbase + (int64_t)(kb_ >> 5) * 32 * HD + lane * 8;                                   \
+    const bf16_t* vt = vbase + (int64_t)(kb_ >> 5) * HD * 32 + lane * 8;                                   \
+    _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                                        \
+      __builtin_amdgcn_global_load_lds((const void*)(kt + (2 * wave + u) * 512),                          \
+                                       (__attribute__((address_space(3))) void*)&S.k[2 * wave + u][0], 16, 0, 0); \
+      __builtin_amdgcn_global_load_lds((const void*)(vt + (2 * wave + u) * 512),                          \
+                                       (__attribute__((address_space(3))) void*)&S.v[64 * (2 * wave + u)], 16, 0, 0); \
+    }                                                                                                      \
+  }
+#define PF_SYNC()                                                                                          \
+  {                                                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                                     \
+    __builtin_amdgcn_s_waitcnt((4 & 15) | (7 << 4) | (0 << 8)); /* vmcnt(4): the next tile may be in flight */ \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                                     \
+    __builtin_amdgcn_s_barrier();                                                                          \
+    __builtin_amdgcn_sched_barrier(0);                                                                     \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                               \
+  }
+#define PF_TILE(S, t_)                                                                                     \
+  {                                                                                                        \
+    const int kb = t0 + 32 * (t_);                                                                         \
+    if (wact && kb <= w_hi && kb + 31 >= w_lo) {                                                           \
+      f32x16 sa, sb;                                                                                       \
+      _Pragma("unroll") for (int x = 0; x < 16; ++x) { sa[x] = 0.f; sb[x] = 0.f; }                       \
+      _Pragma("unroll") for (int h = 0; h < 8; ++h) {                                                      \
+        const int gq = (2 * h + hl) & 3;                                                                   \
+        const v4u kf = __builtin_bit_cast(v4u, S.k[2 * (h >> 1) + kcc][kr + 16 * gq]);                    \
+        if (h & 1) sb = mfma32(kf, qf[h], sb);                                                             \
+        else sa = mfma32(kf, qf[h], sa);                                                                   \
+      }                                                                                                    \
+      float pv[16];                                                                                        \
+      float mt = -INFINITY;                                                                                \
+      if (wfull && kb >= w_full_lo && kb + 31 <= w_full_hi) {                                              \
+        _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                                   \
+          pv[i] = (sa[i] + sb[i]) * scale_log2;                                                            \
+          mt = fmaxf(mt, pv[i]);                                                                           \
+        }                                                                                                  \
+      } else {                                                                                             \
+        _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                                   \
+          const int key = kb + 8 * (i >> 2) + 4 * hl + (i & 3);                                            \
+          const bool ok = cvalid && key >= lo_c && key <= pos_c;                                           \
+          pv[i] = ok ? (sa[i] + sb[i]) * scale_log2 : -INFINITY;                                           \
+          mt = fmaxf(mt, pv[i]);                                                                           \
+        }                                                                                                  \
+      }                                                                                                    \
+      mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));                                                            \
+      const float m_new = fmaxf(m_run, mt);                                                                \
+      float alpha = 1.f, psum = 0.f;                                                                       \
+      if (m_new == -INFINITY) {                                                                            \
+        _Pragma("unroll") for (int i = 0; i < 16; ++i) pv[i] = 0.f;                                        \
+      } else {                                                                                             \
+        alpha = __builtin_amdgcn_exp2f(m_run - m_new);                                                     \
+        _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                                   \
+          pv[i] = __builtin_amdgcn_exp2f(pv[i] - m_new);                                                   \
+          psum += pv[i];                                                                                   \
+        }                                                                                                  \
+      }                                                                                                    \
+      l_run = l_run * alpha + psum;                                                                        \
+      m_run = m_new;                                                                                       \
+      uint2 pk[4];                                                                                         \
+      _Pragma("unroll") for (int g4 = 0; g4 < 4; ++g4)                                                     \
+        pk[g4] = uint2{pack2bf(pv[4 * g4], pv[4 * g4 + 1]), pack2bf(pv[4 * g4 + 2], pv[4 * g4 + 3])};    \
+      _Pragma("unroll") for (int dd = 0; dd < 4; ++dd) O[dd] *= alpha;                                     \
+      _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                   \
+        const uint2 mine = pk[2 * kh + hl], give = pk[2 * kh + 1 - hl];                                    \
+        uint2 got;                                                                                         \
+        got.x = __shfl_xor(give.x, 32, WAVE);                                                              \
+        got.y = __shfl_xor(give.y, 32, WAVE);                                                              \
+        const v4u pb = hl == 0 ? v4u{mine.x, mine.y, got.x, got.y} : v4u{got.x, got.y, mine.x, mine.y};    \
+        _Pragma("unroll") for (int dd = 0; dd < 4; ++dd) {                                                 \
+          const v4u vf = __builtin_bit_cast(v4u, S.v[(32 * dd + kk) * 4 + 2 * kh + hl]);                  \
+          O[dd] = mfma32(vf, pb, O[dd]);                                                                   \
+        }                                                                                                  \
+      }                                                                                                    \
+    }                                                                                                      \
+  }
+  PF_ISSUE(st0, 0);
+  PF_ISSUE(st1, 1);
+  int t = 0;
+#define PF_STEP(SC, SI, t_)                                                                                \
+  {                                                                                                        \
+    PF_SYNC();                                                                                             \
+    PF_TILE(SC, t_);                                                                                       \
+    PF_ISSUE(SI, (t_) + 2);                                                                                \
+  }
+  for (; t + 2 < ntiles; t += 3) {
+    PF_STEP(st0, st2, t);
+    PF_STEP(st1, st0, t + 1);
+    PF_STEP(st2, st1, t + 2);
+  }
+  if (t < ntiles) PF_STEP(st0, st2, t);
+  if (t + 1 < ntiles) PF_STEP(st1, st0, t + 1);
+#undef PF_STEP
+#undef PF_TILE
+#undef PF_SYNC
+#undef PF_ISSUE
+  __builtin_amdgcn_s_waitcnt(0);  // no direct load outlives the workgroup's LDS
+  if (!cvalid) return;
+  const float l_tot = l_run + __shfl_xor(l_run, 32, WAVE);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  // lane: column l % 32; register 4 i4 + x of O[dd] is dim 32 dd + 8 i4 + 4 hl + x
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
       uint2 pk;
-      pk.x = pack2bf(O[u][db][0] * inv, O[u][db][1] * inv);
-      pk.y = pack2bf(O[u][db][2] * inv, O[u][db][3] * inv);
-      *(uint2*)(y + frag_idx(base + j_c[u], head_c[u] * HD + 16 * db + 4 * g4, H * HD)) = pk;
+      pk.x = pack2bf(O[dd][4 * i4] * inv, O[dd][4 * i4 + 1] * inv);
+      pk.y = pack2bf(O[dd][4 * i4 + 2] * inv, O[dd][4 * i4 + 3] * inv);
+      *(uint2*)(y + frag_idx(base + j, head * HD + 32 * dd + 8 * i4 + 4 * hl, H * HD)) = pk;
     }
-  }
 }
 
 // One workgroup per (row, KV group, query block): merge the key splits of
@@ -722,7 +795,7 @@ __global__ __launch_bounds__(256) void k_attn_valu(const T* __restrict__ q, cons
 #ifndef FC_ATTN_TARGET_WG
 #define FC_ATTN_TARGET_WG 256
 #endif
-// query columns per row from which a chunk takes k_attn_chunk
+// query columns per row from which a chunk takes the prefill kernel
 #ifndef FC_ATTN_CHUNK_COLS
 #define FC_ATTN_CHUNK_COLS 128
 #endif
@@ -771,13 +844,12 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
   FC_CHECK_ARG(max_per_row > 0, "max_per_row");
   const float scale = 1.f / sqrtf((float)hd);
   if (dtype == FC_BF16 && hd == 128 && typ_per_row * (H / G) >= FC_ATTN_CHUNK_COLS) {
-    // prefill-width chunks: QB query blocks per wave, 4 waves per workgroup
-    constexpr int QB = 2;
-    const int nqblk = (max_per_row * (H / G) + 15) / 16;
     FC_CHECK_ARG(B * G <= 65535, "batch * n_kv_head must be <= 65535");
-    hipLaunchKernelGGL(k_attn_chunk<QB>, dim3((nqblk + 4 * QB - 1) / (4 * QB), B * G), dim3(256), 0, s,
-                       (const bf16_t*)q, (const bf16_t*)kc, (const bf16_t*)vc, (bf16_t*)y, H, G, cap, row_off, start,
-                       max_per_row, max_tokens, window, scale * 1.4426950408889634f);
+    const int ncolmax = max_per_row * (H / G);
+    // prefill-width chunks: 128 query columns per workgroup, 32x32x16 MFMA
+    hipLaunchKernelGGL(k_attn_pf, dim3((ncolmax + 127) / 128, B * G), dim3(256), 0, s, (const bf16_t*)q,
+                       (const bf16_t*)kc, (const bf16_t*)vc, (bf16_t*)y, H, G, cap, row_off, start, max_per_row,
+                       max_tokens, window, scale * 1.4426950408889634f);
   } else if (dtype == FC_BF16 && hd == 128) {
     AttnGrid a = fc_attn_grid(B, max_per_row, typ_per_row, H, G, max_keys);
     const int64_t units = (int64_t)B * G * a.nqblk * a.nsplit * 16;

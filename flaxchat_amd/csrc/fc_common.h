@@ -10,6 +10,16 @@
 typedef uint16_t bf16_t;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// bf16 MFMA 32x32x16 (gfx950): lane l holds row / column l % 32 and k values
+// 8 (l / 32) .. +7 of each operand; the result register 4 i + x of lane l is
+// row 8 i + 4 (l / 32) + x, column l % 32.
+__device__ __forceinline__ f32x16 mfma32(v4u a, v4u b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+}
 
 #define WAVE 64
 

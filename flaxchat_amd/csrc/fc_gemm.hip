@@ -169,7 +169,6 @@ __global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* 
 // A / column (l % 16) of B and 8 consecutive k values 8*(l/16)..+7 of a
 // 32-wide k step; the f32x4 result holds rows 4*(l/16)+i of column l % 16.
 // ---------------------------------------------------------------------------
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 // weight fragment loads: plain (they are re-read across M tiles through L2)
 #define W_LD(p) (*(p))
 // lm_head weights (the softcap epilogue) always stream non-temporally: the
@@ -786,11 +785,6 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
 #ifndef FC_BIG_MIN_TILES
 #define FC_BIG_MIN_TILES 224
 #endif
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-__device__ __forceinline__ f32x16 mfma32(v4u a, v4u b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                  0, 0);
-}
 template <int NB>
 struct BigStage {
   uint4 a[16][64];
