@@ -383,26 +383,72 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
 // value-embedding gate; q goes to q[m][head], k / v to the cache at the
 // token's position. Eight consecutive lanes share a token (`part` = which
 // 8 rotary pairs); all 8 take part in the norm's shuffles.
-__device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int m, int M, int hh, int part) {
+//
+// The inputs that do not depend on the GEMM result are loaded first, in two
+// steps that callers issue ahead of the accumulator staging so the loads of
+// several tokens are in flight together: qkv_pre_row (the token's cache row,
+// position and id) and qkv_pre_tab (the rotary table entries of the q / k
+// heads; the value-embedding slice and the gate inputs of the v heads).
+struct QkvPre {
+  int b, pos, tok;
+  float c[8], s[8];  // q / k heads: cos / sin of the lane's 8 rotary pairs
+  uint4 h0, ve0, ve1;  // v heads: A row k 0..7, ve dims 8 part .. +7 and 64 + 8 part .. +7
+  uint2 h1;            // v heads: A row k 8..11
+};
+
+__device__ __forceinline__ void qkv_pre_row(const QkvEpi& Q, int m, int M, int hh, QkvPre& p) {
+  p.b = 0;
+  p.pos = 0;
+  p.tok = 0;
+  if (m < M) {
+    p.b = Q.tok_row[m];
+    p.pos = Q.tok_pos[m];
+    if (hh >= Q.H + Q.G && Q.ve != nullptr) p.tok = Q.tokens[m];
+  }
+}
+
+__device__ __forceinline__ void qkv_pre_tab(const QkvEpi& Q, int m, int M, int hh, int part, QkvPre& p) {
+  if (hh < Q.H + Q.G) {
+    const int pc = min(max(p.pos, 0), Q.rope_len - 1);
+    const float4* cp = (const float4*)(Q.rcos + (int64_t)pc * 64 + 8 * part);
+    const float4* sp = (const float4*)(Q.rsin + (int64_t)pc * 64 + 8 * part);
+    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    p.c[0] = c0.x; p.c[1] = c0.y; p.c[2] = c0.z; p.c[3] = c0.w;
+    p.c[4] = c1.x; p.c[5] = c1.y; p.c[6] = c1.z; p.c[7] = c1.w;
+    p.s[0] = s0.x; p.s[1] = s0.y; p.s[2] = s0.z; p.s[3] = s0.w;
+    p.s[4] = s1.x; p.s[5] = s1.y; p.s[6] = s1.z; p.s[7] = s1.w;
+  } else if (Q.ve != nullptr && m < M) {
+    // A row m, k 0..7 then 8..11: 16 contiguous bytes each in fragment order
+    const uint16_t* hr = Q.h + frag_idx(m, 0, Q.D);
+    p.h0 = *(const uint4*)hr;
+    p.h1 = *(const uint2*)(hr + 128);
+    const uint16_t* vr = Q.ve + ((int64_t)p.tok * Q.G + (hh - Q.H - Q.G)) * 128;
+    p.ve0 = *(const uint4*)(vr + 8 * part);
+    p.ve1 = *(const uint4*)(vr + 64 + 8 * part);
+  }
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int m, int M, int hh, int part,
+                                           const QkvPre& p) {
   const bool live = m < M;
   float x1[8], x2[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    x1[e] = x[8 * part + e];
-    x2[e] = x[64 + 8 * part + e];
+  {
+    const float4* xa = (const float4*)(x + 8 * part);
+    const float4* xb = (const float4*)(x + 64 + 8 * part);
+    const float4 a0 = xa[0], a1 = xa[1], b0 = xb[0], b1 = xb[1];
+    x1[0] = a0.x; x1[1] = a0.y; x1[2] = a0.z; x1[3] = a0.w; x1[4] = a1.x; x1[5] = a1.y; x1[6] = a1.z; x1[7] = a1.w;
+    x2[0] = b0.x; x2[1] = b0.y; x2[2] = b0.z; x2[3] = b0.w; x2[4] = b1.x; x2[5] = b1.y; x2[6] = b1.z; x2[7] = b1.w;
   }
-  int b = 0, pos = 0;
-  if (live) {
-    b = Q.tok_row[m];
-    pos = Q.tok_pos[m];
-  }
+  const int b = p.b, pos = p.pos;
   const bool in_cache = live && (unsigned)b < (unsigned)Q.B && pos >= 0 && pos < Q.cap;
   if (hh < Q.H + Q.G) {
-    const int pc = min(max(pos, 0), Q.rope_len - 1);
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float c = Q.rcos[(int64_t)pc * 64 + 8 * part + e], s = Q.rsin[(int64_t)pc * 64 + 8 * part + e];
+      const float c = p.c[e], s = p.s[e];
       const float y1 = x1[e] * c + x2[e] * s;
       const float y2 = x1[e] * (-s) + x2[e] * c;
       x1[e] = y1;
@@ -435,15 +481,22 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
   } else {
     const int gv = hh - Q.H - Q.G;
     if (Q.ve != nullptr && live) {
+      const uint32_t hw[6] = {p.h0.x, p.h0.y, p.h0.z, p.h0.w, p.h1.x, p.h1.y};
+      const float* wg = Q.ve_gate + gv * 12;
       float z = 0.f;
 #pragma unroll
-      for (int i = 0; i < 12; ++i) z += bf2f(Q.h[frag_idx(m, i, Q.D)]) * Q.ve_gate[gv * 12 + i];
+      for (int i = 0; i < 6; ++i) {
+        z += bf_lo(hw[i]) * wg[2 * i];
+        z += bf_hi(hw[i]) * wg[2 * i + 1];
+      }
       const float gate = 3.f * (1.f / (1.f + expf(-z)));
-      const bf16_t* vr = Q.ve + ((int64_t)Q.tokens[m] * Q.G + gv) * 128;
+      const uint32_t va[4] = {p.ve0.x, p.ve0.y, p.ve0.z, p.ve0.w}, vb[4] = {p.ve1.x, p.ve1.y, p.ve1.z, p.ve1.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x1[e] = x1[e] + gate * bf2f(vr[8 * part + e]);
-        x2[e] = x2[e] + gate * bf2f(vr[64 + 8 * part + e]);
+      for (int e = 0; e < 4; ++e) {
+        x1[2 * e] = x1[2 * e] + gate * bf_lo(va[e]);
+        x1[2 * e + 1] = x1[2 * e + 1] + gate * bf_hi(va[e]);
+        x2[2 * e] = x2[2 * e] + gate * bf_lo(vb[e]);
+        x2[2 * e + 1] = x2[2 * e + 1] + gate * bf_hi(vb[e]);
       }
     }
     if (in_cache) {
@@ -460,8 +513,8 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
 // Epilogue of the column-split kernels (k_gemm_la, k_gemm_dma): acc[mb][j]
 // holds rows 16 mb + 4 g + i, column 16 (wave NBW + j) + r of the tile.
 template <int MB, int NBW, int EPI>
-__device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[MB][NBW], const RmsPre& rpre, int m0,
-                                              int n0, int nt, int s, int M, int K) {
+__device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[MB][NBW], const RmsPre& rpre,
+                                              QkvPre& qpre, int m0, int n0, int nt, int s, int M, int K) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   if constexpr (EPI == EPI_QKV) {
@@ -470,6 +523,7 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[M
     // d + 64 of 8 rotary pairs)
     static_assert(MB == 2 && NBW == 2, "EPI_QKV needs 32 x 128 tiles");
     __shared__ float T[32][128 + 4];
+    qkv_pre_tab(e.qkv, m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7, qpre);  // in flight while staging
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -477,7 +531,7 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[M
 #pragma unroll
         for (int i = 0; i < 4; ++i) T[16 * mb + 4 * g + i][16 * (wave * NBW + j) + r] = acc[mb][j][i];
     __syncthreads();
-    qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7);
+    qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7, qpre);
   } else {
     // folded RMSNorm (RELU2 reading the bf16 copy of x): acc row
     // 16 mb + 4 g + i takes the factor lane 4 g + i computed for its row
@@ -574,6 +628,8 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
   if constexpr (EPI == EPI_RELU2) {
     if (e.rms_in != nullptr) rms_load<16 * MB>(rpre, e, m0, M);
   }
+  QkvPre qpre;  // EPI_QKV: the cache row / position of this thread's token (row m0 + t / 8)
+  if constexpr (EPI == EPI_QKV) qkv_pre_row(e.qkv, m0 + (threadIdx.x >> 3), M, nt, qpre);
   f32x4 acc[MB][NBW];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -630,7 +686,7 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #undef LA_STAGE_A
   }
 
-  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, m0, n0, nt, s, M, K);
+  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, qpre, m0, n0, nt, s, M, K);
 }
 
 // bf16 MFMA GEMM for verify-size row counts with both operands staged in an
@@ -688,9 +744,10 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
     abase[u] = A + ((int64_t)min(m0 / 16 + (q >> 1), last_blk) * KS32 + (q & 1)) * 512 + lane * 8;
   }
   RmsPre rpre;  // folded RMSNorm: this thread's share of row m0 + t / (256 / MT)
-  if constexpr (EPI == EPI_RELU2 || EPI == EPI_QKV) {
+  if constexpr (EPI == EPI_RELU2) {
     if (e.rms_in != nullptr) rms_load<16 * MB>(rpre, e, m0, M);
   }
+  QkvPre qpre;  // unused: the fused QKV epilogue runs on k_gemm_la and k_gemm_big
   f32x4 acc[MB][NBW];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -746,7 +803,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
 #undef DMA_ISSUE
   __builtin_amdgcn_s_waitcnt(0);  // no direct load outlives the workgroup's LDS
   __syncthreads();                // the epilogue may reuse LDS
-  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, m0, n0, nt, 0, M, K);
+  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, qpre, m0, n0, nt, 0, M, K);
 }
 
 // bf16 MFMA GEMM for prefill-size row counts (M >= FC_BIG_M, N % 256 == 0,
@@ -958,8 +1015,28 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
     BigStage<NB>* mine = wave == 0 ? &s0 : wave == 1 ? &s1 : wave == 2 ? &s2 : &s3;
     float(*T)[128 + 4] = (float(*)[128 + 4])mine;
     const int hh = (n0 + 128 * wn) >> 7;
+    const int mq = m0 + 128 * wm + (lane >> 3);  // this lane's token in group p, step it: mq + 32 p + 8 it
+    int rb[4][4], rp[4][4], rt[4][4];             // their cache rows / positions / ids, loaded together
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        QkvPre r;
+        qkv_pre_row(e.qkv, mq + 32 * p + 8 * it, M, hh, r);
+        rb[p][it] = r.b;
+        rp[p][it] = r.pos;
+        rt[p][it] = r.tok;
+      }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
+      QkvPre pre[4];  // table / value-embedding loads of the group's 4 tokens, in flight while it is staged
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        pre[it].b = rb[p][it];
+        pre[it].pos = rp[p][it];
+        pre[it].tok = rt[p][it];
+        qkv_pre_tab(e.qkv, mq + 32 * p + 8 * it, M, hh, lane & 7, pre[it]);
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -970,7 +1047,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int tt = 8 * it + (lane >> 3);
-        qkv_finish(e.qkv, T[tt], m0 + 128 * wm + 32 * p + tt, M, hh, lane & 7);
+        qkv_finish(e.qkv, T[tt], m0 + 128 * wm + 32 * p + tt, M, hh, lane & 7, pre[it]);
       }
       __builtin_amdgcn_wave_barrier();
     }
