@@ -631,9 +631,35 @@ __device__ __forceinline__ void load4(const float* __restrict__ z, int e, int V,
   }
 }
 
-// Block-wide (value, index) argmax for a VP_THR block; result in thread 0.
+// Block-wide (value, index) argmax for a VP_THR block; result in every thread.
 __device__ __forceinline__ void vp_argmax(float& v, int& i, float* redv, int* redi) {
   block_argmax(v, i, redv, redi);
+}
+
+// Two block-wide argmaxes through one LDS exchange (redv / redi hold 2 x the
+// wave count); each result equals what vp_argmax returns for it.
+__device__ __forceinline__ void vp_argmax2(float& v, int& i, float& u, int& j, float* redv, int* redi) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = VP_THR / 64;
+  wave_argmax(v, i);
+  wave_argmax(u, j);
+  __syncthreads();
+  if (lane == 0) {
+    redv[w] = v;
+    redi[w] = i;
+    redv[nw + w] = u;
+    redi[nw + w] = j;
+  }
+  __syncthreads();
+  float bv = redv[0], bu = redv[nw];
+  int bi = redi[0], bj = redi[nw];
+  for (int k = 1; k < nw; ++k) {
+    argmax_merge(bv, bi, redv[k], redi[k]);
+    argmax_merge(bu, bj, redv[nw + k], redi[nw + k]);
+  }
+  v = bv;
+  i = bi;
+  u = bu;
+  j = bj;
 }
 
 // Chunk partials of rows r of z0 (row stride `row_stride` floats): argmax,
@@ -670,15 +696,13 @@ __global__ __launch_bounds__(VP_THR) void k_vpart(const float* __restrict__ z0, 
   p.g = -INFINITY;
   p.gi = 0x7fffffff;
   if (T > 0.f) {
-    float m = -INFINITY;
+    // max of z / T is max(z) / T exactly (division by T > 0 is monotone
+    // under round-to-nearest), so the argmax reduction above gives it
+    const float m = bz / T;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        v[j][w] = v[j][w] / T;
-        if (e0[j] + w < V) m = fmaxf(m, v[j][w]);
-      }
-    m = block_max(m, redv);
+      for (int w = 0; w < 4; ++w) v[j][w] = v[j][w] / T;
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -706,8 +730,7 @@ __global__ __launch_bounds__(VP_THR) void k_vpart(const float* __restrict__ z0, 
           argmax_merge(bg, bgi, G, i);
         }
       }
-      vp_argmax(ba, bai, redv, redi);
-      vp_argmax(bg, bgi, redv, redi);
+      vp_argmax2(ba, bai, bg, bgi, redv, redi);
       p.a = ba;
       p.ai = bai;
       p.g = bg;
