@@ -984,7 +984,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
   BIG_ISSUE(s1, 1);
   BIG_ISSUE(s2, 2);
   BIG_ISSUE(s3, 3);
-  BIG_SYNC(3 * 8);  // chunk 0 landed
+  BIG_SYNC(3 * (4 + NB));  // chunk 0 landed: at most the 3 later chunks' loads outstanding
   BIG_READ(s0, wf0, af0);
   // C % 4 == 0 (K % 128 == 0): 4-step groups, the last one ends without a read
   int i = 0;
