@@ -174,6 +174,8 @@ def _to_kblocked(K):
     (3, 130, 12, 4, 300, 900),  # the same, GQA 3:1 (390 columns) and a window
     (2, 256, 4, 4, 64, 700),    # short window: blocks skip the tiles they cannot see
     (4, 200, 6, 2, 0, 500),     # ragged rows, GQA 3:1
+    (64, 5, 6, 6, 1024, 2048),  # the config-3 microbenchmark shape: 64 rows x 5 queries, sliding-window layer
+    (64, 5, 6, 6, 0, 2048),     # the same, full layer
 ])
 def test_attention_parity(dtype, B, W, H, G, window, lmax):
     _say(f"attention dtype={dtype} B={B} W={W} H={H} G={G} window={window} lmax={lmax}")
@@ -253,3 +255,57 @@ def test_row_stats(V, top_k, T):
         x = (z[r][keep] / np.float32(T)).astype(np.float32)
         assert np.float32(rs.mx) == x.max()
         np.testing.assert_allclose(rs.sum, np.exp(x.astype(np.float64) - x.max()).sum(), rtol=1e-5)
+
+
+# ---------------------------------------------------------------- accept at full vocabulary
+@pytest.mark.parametrize("T", [1.0, 0.0])
+def test_spec_accept_cfg3_vs_oracle(T):
+    """fc_spec_accept on the config-3 sampling shape (64 rows, k = 4, V =
+    65536: the vocab-wide passes run in 64 chunks per row and merge their
+    partials) against the oracle's accept_round (flaxchat/engine.py:525-592)
+    on the same logits, drafts and Philox counters. Target logits are
+    15 tanh(N(0, 2^2) / 15), the draft's the target's plus N(0, 0.5^2)
+    noise (softcapped again); drafts are the oracle's own draws from the
+    draft logits. The emitted tokens must match exactly."""
+    from oracle import sampling as S
+    _say(f"spec accept cfg3 T={T}")
+    B, k, V, seed = 64, 4, 65536, 1234
+    rng = np.random.default_rng(11)
+    P = (15 * np.tanh(rng.standard_normal((B, k + 1, V)) * 2 / 15)).astype(np.float32)
+    Q = (15 * np.tanh((P[:, :k] + rng.standard_normal((B, k, V)) * 0.5) / 15)).astype(np.float32)
+    rnd = (np.arange(B) % 5).astype(np.int32)
+    drafts = np.array([[S.draft_sample(Q[b, i], T, None, seed, b, int(rnd[b]), i) for i in range(k)]
+                       for b in range(B)], np.int32)
+    i32 = dict(dtype=torch.int32, device=dev())
+    z = lambda *s: torch.zeros(*s, **i32)  # noqa: E731
+    gen_cap, P_MAX = 64, _lib.PMAX
+    bufs = dict(t_len=torch.full((B,), 10, **i32), d_len=torch.full((B,), 10, **i32), t_pend=z(B, P_MAX),
+                d_pend=z(B, P_MAX), t_pend_n=torch.ones(B, **i32), d_pend_n=torch.ones(B, **i32),
+                t_dirty=torch.full((B,), 1 << 30, **i32), d_dirty=torch.full((B,), 1 << 30, **i32),
+                gen=z(B, gen_cap), gen_n=torch.full((B,), 11, **i32), prompt_len=torch.full((B,), 11, **i32),
+                round=torch.from_numpy(rnd).to(dev()), stall=z(B), result=z(B, _lib.RES_STRIDE),
+                tok_d0=z(B * P_MAX), off_d0=z(B + 1), start_d=z(k, B), tok_ds=z(k, B), off_ds=z(B + 1),
+                tok_v=z(B * (P_MAX + k)), off_v=z(B + 1), start_v=z(B), drafts=torch.from_numpy(drafts).to(dev()),
+                q_logits=torch.from_numpy(Q).to(dev()), p_logits=torch.from_numpy(P).to(dev()),
+                q_stats=torch.zeros(B * k * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev()),
+                p_stats=torch.zeros(B * (k + 1) * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev()),
+                part=torch.zeros(lib().fc_spec_part_bytes(B, k, V), dtype=torch.uint8, device=dev()))
+    st = _lib.FcSpecState(B, k, 40, gen_cap, V, T, 0, seed, *[bufs[n].data_ptr() for n in _lib._SPEC_PTRS],
+                          bufs["part"].data_ptr(), bufs["part"].numel())
+    # the draft's row statistics come from the draft steps in a round; here from fc_row_stats
+    check(lib().fc_row_stats(bufs["q_logits"].data_ptr(), B * k, V, T, 0, bufs["q_stats"].data_ptr(), stream()),
+          "row stats")
+    check(lib().fc_spec_accept(ctypes.byref(st), stream()), "spec accept")
+    torch.cuda.synchronize()
+    res = bufs["result"].cpu().numpy()
+    assert np.array_equal(bufs["round"].cpu().numpy(), rnd + 1)
+    n_acc = n_bonus = 0
+    for b in range(B):
+        em, acc, rej, bonus = S.accept_round(P[b], Q[b], drafts[b], T, None, seed, b, int(rnd[b]))
+        n = int(res[b, 0])
+        assert res[b, 8:8 + n].tolist() == em, f"row {b}: {res[b, 8:8 + n].tolist()} vs oracle {em}"
+        assert (int(res[b, 1]), int(res[b, 2])) == (acc, rej), f"row {b}"
+        n_acc += acc
+        n_bonus += bonus
+    _say(f"accepted {n_acc} of {B * k}, bonus rows {n_bonus}")
+    assert 0 < n_bonus < B  # both the bonus and the rejection paths ran
