@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
   const int64_t item = (int64_t)blockIdx.x * 4 + wave;
   if (item >= (int64_t)Mcap * NH) return;
   const int m = (int)(item / NH), hh = (int)(item % NH);
-  if (m >= *Mdev) return;
+  if (Mdev != nullptr && m >= *Mdev) return;
   const int b = tok_row[m], pos = tok_pos[m];
   if ((unsigned)b >= (unsigned)B) return;
   const int half = hd >> 1;
@@ -137,6 +137,19 @@ int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
+}
+
+extern "C" int32_t fc_attn_prologue(const fc_model* m, int32_t layer, const fc_cache* c, const float* qkv,
+                                    const void* h, const int32_t* tokens, const int32_t* tok_row,
+                                    const int32_t* tok_pos, int32_t M, void* q, void* stream) {
+  FC_CHECK_ARG(m && c && qkv && h && tokens && tok_row && tok_pos && q, "null pointer");
+  FC_CHECK_ARG(layer >= 0 && layer < m->n_layer && m->layers != nullptr, "layer out of range");
+  FC_CHECK_ARG(m->dtype == FC_F32 || m->dtype == FC_BF16, "dtype");
+  FC_CHECK_ARG(m->n_head > 0 && m->n_kv_head > 0 && m->n_head % m->n_kv_head == 0, "head counts");
+  FC_CHECK_ARG(c->k && c->v && c->batch > 0 && c->cap > 0 && c->cap % 32 == 0, "cache");
+  FC_CHECK_ARG(M >= 0, "M");
+  if (M == 0) return FC_OK;
+  return fc_launch_prologue(qkv, h, tokens, m, layer, c, tok_row, tok_pos, M, nullptr, q, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -215,6 +215,20 @@ int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y,
                      const int32_t* start, int32_t window, int32_t max_keys, int32_t dtype, void* work,
                      int64_t work_bytes, void* stream);
 
+/* Attention prologue of one layer for M packed tokens (flaxchat/engine.py:96-126,
+ * flaxchat/gpt.py:52-71; the piece fc_forward runs between the QKV GEMM and the
+ * attention). qkv: the QKV GEMM output, fp32 [M][(H + 2G) * head_dim] (q heads,
+ * then k, then v). q and k heads: RoPE at position tok_pos[m] (the model's
+ * tables), then 1.2 * RMSNorm (eps 1e-6). v heads of a layer with a value
+ * embedding: v + 3 sigmoid(h[m][0:12] . ve_gate[g]) * ve[tokens[m]][g]. h is the
+ * QKV GEMM's input (bf16: fragment order over round16(M) rows; fp32: row-major
+ * [M][n_embd]). q -> q[m][H][head_dim] in the model dtype; k and v are written
+ * into row tok_row[m] (< batch) of the layer's cache at tok_pos[m] when it lies
+ * in [0, cap); tokens with tok_row[m] outside [0, batch) are skipped. */
+int32_t fc_attn_prologue(const fc_model* m, int32_t layer, const fc_cache* c, const float* qkv,
+                         const void* h, const int32_t* tokens, const int32_t* tok_row,
+                         const int32_t* tok_pos, int32_t M, void* q, void* stream);
+
 /* Per-row statistics of fp32 logits rows (flaxchat/engine.py:461-476):
  * lax.top_k keep-set (exactly k, lower index first among ties), max and
  * softmax normaliser of z/T over it, and the first-index argmax. */

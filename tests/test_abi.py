@@ -45,6 +45,9 @@ def test_argument_errors_are_status_codes():
     assert rc == -1
     st = _lib.FcSpecState()
     assert L.fc_spec_accept(ctypes.byref(st), None) == -1
+    m, c = _lib.FcModel(), _lib.FcCache()
+    assert L.fc_attn_prologue(ctypes.byref(m), 0, ctypes.byref(c), None, None, None, None, None, 1, None, None) == -1
+    assert b"null" in L.fc_last_error()
 
 
 def test_struct_layout_matches_c(tmp_path):

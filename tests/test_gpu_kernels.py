@@ -309,3 +309,76 @@ def test_spec_accept_cfg3_vs_oracle(T):
         n_bonus += bonus
     _say(f"accepted {n_acc} of {B * k}, bonus rows {n_bonus}")
     assert 0 < n_bonus < B  # both the bonus and the rejection paths ran
+
+
+# ---------------------------------------------------------------- attention prologue
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_attn_prologue_vs_oracle(dtype):
+    """fc_attn_prologue against the oracle's per-token prologue
+    (oracle/model.py Oracle.step: apply_rotary_emb, rms_norm * 1.2, the
+    value-embedding gate 3 sigmoid(h[:12] . ve_gate)) on GQA heads (4 q, 2
+    kv), for a layer without a value embedding (0) and one with (1); cache
+    positions at both ends, and one at cap (q written, nothing appended).
+    bf16: the inputs the device holds in bf16 (h, the VE table) are rounded
+    first; tolerance 2e-2 (outputs rounded to bf16), fp32 1e-5."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    from flaxchat_amd.runtime import DeviceCache, DeviceModel
+    from oracle.model import apply_rotary_emb, rms_norm, sigmoid
+    _say(f"attention prologue {dtype}")
+    H, G, d, D, V = 4, 2, 128, 512, 512
+    cfg = GPTConfig(sequence_len=128, vocab_size=V, n_layer=2, n_head=H, n_kv_head=G, n_embd=D,
+                    window_pattern="SL", short_window=64)
+    host = GPT.init_normal(cfg, seed=3, std=0.1)
+    dm = DeviceModel.from_host(host, dtype=dtype, device=dev())
+    B, cap = 3, 96
+    cache = DeviceCache(dm, B, cap)
+    rows = np.array([0, 0, 1, 2, 2, 2, 1, 0], np.int32)
+    pos = np.array([5, 6, 40, 0, 1, 95, 41, 96], np.int32)
+    M = len(rows)
+    rng = np.random.default_rng(7)
+    tokens = rng.integers(0, V, M).astype(np.int32)
+    qkv = rng.standard_normal((M, (H + 2 * G) * d)).astype(np.float32)
+    hrow = rng.standard_normal((M, D)).astype(np.float32)
+    tdt = torch.float32 if dtype == "fp32" else torch.bfloat16
+    if dtype == "bf16":
+        from flaxchat_amd.runtime import frag_pack
+        hrow = bf(hrow)
+        h_t = torch.from_numpy(frag_pack(hrow)).to(dev(), tdt)
+    else:
+        h_t = torch.from_numpy(hrow).to(dev())
+    cos, sin = dm.t["rope_cos"].cpu().numpy(), dm.t["rope_sin"].cpu().numpy()
+    i32 = lambda a: torch.from_numpy(a).to(dev())  # noqa: E731
+    qkv_t, tok_t, row_t, pos_t = i32(qkv), i32(tokens), i32(rows), i32(pos)
+    tol = 1e-5 if dtype == "fp32" else 2e-2
+    for layer in range(2):
+        q = torch.zeros(M, H, d, dtype=tdt, device=dev())
+        check(lib().fc_attn_prologue(ctypes.byref(dm.desc), layer, ctypes.byref(cache.desc), qkv_t.data_ptr(),
+                                     h_t.data_ptr(), tok_t.data_ptr(), row_t.data_ptr(), pos_t.data_ptr(), M,
+                                     q.data_ptr(), stream()), "attn prologue")
+        torch.cuda.synchronize()
+        ve = host.value_embeds.get(str(layer))
+        assert (ve is not None) == (layer == 1)
+        q_ref = np.zeros((M, H, d), np.float32)
+        k_nat = np.zeros((B, G, cap, d), np.float32)
+        v_nat = np.zeros((B, G, cap, d), np.float32)
+        for m in range(M):
+            c, s_ = cos[pos[m]], sin[pos[m]]
+            q_ref[m] = rms_norm(apply_rotary_emb(qkv[m, :H * d].reshape(H, d), c, s_)) * np.float32(1.2)
+            k = rms_norm(apply_rotary_emb(qkv[m, H * d:(H + G) * d].reshape(G, d), c, s_)) * np.float32(1.2)
+            v = qkv[m, (H + G) * d:].reshape(G, d).copy()
+            if ve is not None:
+                emb = ve.embedding[tokens[m]].reshape(G, d).astype(np.float32)
+                if dtype == "bf16":
+                    emb = bf(emb)
+                gv = np.float32(3.0) * sigmoid(hrow[m, :12] @ host.blocks[layer].attn.ve_gate.kernel)
+                v = (v + gv[:, None] * emb).astype(np.float32)
+            if pos[m] < cap:
+                k_nat[rows[m], :, pos[m]] = k
+                v_nat[rows[m], :, pos[m]] = v
+        np.testing.assert_allclose(q.float().cpu().numpy(), q_ref, rtol=tol, atol=tol)
+        k_got = cache.k[layer].float().cpu().numpy()
+        v_got = cache.v[layer].float().cpu().numpy()
+        k_exp = _to_kblocked(k_nat) if dtype == "bf16" else k_nat
+        np.testing.assert_allclose(k_got, k_exp, rtol=tol, atol=tol)
+        np.testing.assert_allclose(v_got, _to_vblocked(v_nat), rtol=tol, atol=tol)
