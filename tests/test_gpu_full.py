@@ -104,3 +104,19 @@ def test_full_forward_rejects_bad_input(tiny_pair):
         gpt_forward(m, [[1, 2, m.config.vocab_size]], dtype="fp32")
     with pytest.raises(ValueError):
         gpt_forward(m, [[1, 2, 3]], [[1, 2]], dtype="fp32")
+
+
+def test_full_forward_bf16_verify_size_split():
+    """n_embd 1024 at 8 x 25 tokens (M = 200, a verify-size chunk): the MLP
+    c_proj (K = 4096) takes the split-K path (32 x 64 tiles, 3 splits) whose
+    partials the RMSNorm kernel sums with the residual update."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    _say("full forward bf16 d1024 8 x 25")
+    cfg = GPTConfig(sequence_len=256, vocab_size=1024, n_layer=2, n_head=8, n_kv_head=8, n_embd=1024,
+                    window_pattern="SL", short_window=64)
+    m = GPT.init_normal(cfg, seed=13, std=0.02).perturb_scalars()
+    ids = np.random.default_rng(13).integers(0, cfg.vocab_size, (8, 25))
+    got = gpt_forward(m, ids, dtype="bf16").cpu().numpy()
+    ref = gpt_call(m, ids)
+    assert np.abs(got - ref).max() < 5e-2
