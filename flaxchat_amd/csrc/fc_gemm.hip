@@ -1238,10 +1238,10 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     const int wgs = N / 64;
     if (can_split && wgs < 256) p.S = std::min((256 + wgs - 1) / wgs, s_max);
   } else if (Mtyp <= 32) {
-    if (!can_split && N >= 16384 && N % 128 == 0) {  // draft lm_head: LDS-shared rows, 128-column tiles
+    if (!can_split && N >= 16384 && N % 64 == 0) {  // draft lm_head: LDS-shared rows, 64-column tiles
       p.la = true;
       p.mb = 2;
-      p.nb = 2;
+      p.nb = 1;
       return p;
     }
     p.mb = 2;
@@ -1349,6 +1349,7 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
     launch_dma<4, 1>(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.la) {
     if (p.mb == 8) launch_la<8, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
+    else if (p.nb == 1) launch_la<2, 1>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
     else launch_la<2, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
   } else if (p.mb == 1) {
     if (p.nb == 4) launch_ks<1, 4, true>(A, W, Mcap, Mdev, N, K, p.S, ee, s);

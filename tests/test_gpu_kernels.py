@@ -52,6 +52,10 @@ def _gemm_cases():
                     if big and (epi in (1, 4) or (dtype == "fp32" and M > 64)):
                         continue
                     cases.append((dtype, M, epi, NK))
+    # draft-size rows with a vocabulary-wide output (the LDS-shared 32 x 64 tiles of the draft lm_head)
+    for M in [20, 32]:
+        for epi in [0, 4]:
+            cases.append(("bf16", M, epi, (16384, 256)))
     # row counts >= 1024 with few output tiles (the 64-row kernels)
     for NK in [(512, 256), (768, 1536)]:
         for M in [1024, 1100, 2304]:
