@@ -1126,9 +1126,9 @@ static void launch_gemv(const void* A, const void* W, int M, const int* Mdev, in
   else launch_gemv_mb<T, 8>(A, W, M, Mdev, N, K, e, s);
 }
 
-// register ring depth of the K-split kernel: 4 chunks for the 32 x 16 tile
-// (few columns, long weight streams per wave), else 3
-template <int MB, int NB, bool PK = false, int NS = (MB == 2 && NB == 1) ? 4 : 3>
+// register ring depth of the K-split kernel: 4 chunks for the 32 x 16 and
+// 32 x 32 tiles (the draft's weight streams: few columns per wave), else 3
+template <int MB, int NB, bool PK = false, int NS = (MB == 2 && NB <= 2) ? 4 : 3>
 static void launch_ks(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int S, const Epi& e,
                       hipStream_t s) {
   const int ntiles = N / (16 * NB), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
