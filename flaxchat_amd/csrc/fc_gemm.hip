@@ -1285,12 +1285,12 @@ bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
 }
 
 // The EPI_ADD GEMM that writes the bf16 copy of x (attention c_proj, bf16):
-// unsplit K-split kernel, 32 x 16 tiles for draft rows, 32 x 64 for verify rows.
+// unsplit K-split kernel, 32 x 16 tiles for draft rows, 32 x 32 for verify rows.
 static GemmPlan plan_fold_add(int Mtyp, int N) {
   GemmPlan p{};
   p.S = 1;
   p.mb = Mtyp <= 16 ? 1 : 2;
-  p.nb = Mtyp <= 16 ? 2 : (Mtyp <= 32 ? 1 : 4);
+  p.nb = Mtyp <= 16 ? 2 : (Mtyp <= 32 ? 1 : 2);
   while (p.nb > 1 && N % (16 * p.nb) != 0) p.nb /= 2;
   if (p.nb == 1 && p.mb != 2) p.nb = 2;
   return p;
