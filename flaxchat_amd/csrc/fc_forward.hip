@@ -254,8 +254,8 @@ static FwdWork carve(const fc_model* m, int B, int max_tokens, int max_per_row, 
   w.part_bytes = fc_attn_part_bytes(B, max_per_row, H, G, hd, 1 << 20);
   w.part = take(w.part_bytes);
   // split-K partials of the two GEMMs that write the residual stream
-  int64_t gp = std::max(fc_gemm_part_bytes(typ_tokens, (int)M, D, H * hd),
-                        fc_gemm_part_bytes(typ_tokens, (int)M, D, 4 * D));
+  int64_t gp = std::max(fc_gemm_part_bytes(typ_tokens, (int)M, D, H * hd, m->dtype),
+                        fc_gemm_part_bytes(typ_tokens, (int)M, D, 4 * D, m->dtype));
   w.gw.part = (float*)take(gp);
   w.gw.part_bytes = gp;
   w.total = off;

@@ -1235,7 +1235,7 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     // one 16-row tile: fill the GPU with column tiles and K splits
     p.mb = 1;
     p.nb = 4;
-    const int wgs = N / 64;
+    const int wgs = std::max(1, N / 64);
     if (can_split && wgs < 256) p.S = std::min((256 + wgs - 1) / wgs, s_max);
   } else if (Mtyp <= 32) {
     if (!can_split && N >= 16384 && N % 64 == 0) {  // draft lm_head: LDS-shared rows, 64-column tiles
@@ -1303,9 +1303,9 @@ bool fc_gemm_fold_ok(int Mtyp, int D) {
   return !c.gemv && !c.big && fc_gemm_fold_tiles(Mtyp, D) <= FC_RMS_REG * (256 / (16 * c.mb));
 }
 
-int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K) {
+int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K, int dtype) {
   if (Mtyp <= 0 || Mcap <= 0 || N <= 0 || K <= 0) return 0;
-  GemmPlan p = plan_gemm(Mtyp, N, K, FC_BF16, true);
+  GemmPlan p = plan_gemm(Mtyp, N, K, dtype, true);  // fp32 GEMMs never split
   return p.S > 1 ? fc_align((int64_t)p.S * Mcap * N * 4) : 0;
 }
 

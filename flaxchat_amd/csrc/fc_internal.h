@@ -57,7 +57,7 @@ struct GemmWork {
   float* part;
   int64_t part_bytes;
 };
-int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K);
+int64_t fc_gemm_part_bytes(int Mtyp, int Mcap, int N, int K, int dtype);
 // column tiles of the EPI_ADD GEMM that writes `xa` (the rms_n of its consumer),
 // and whether its consumers can take that many
 int fc_gemm_fold_tiles(int Mtyp, int N);

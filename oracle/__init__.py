@@ -27,8 +27,12 @@ Pinning (what checks each function, beyond restating the reference):
     norm, RoPE of position 0 is identity, |softcap| < 15).
   * attention: float64 brute force on random tiny inputs; window inclusive
     W+1 keys; chunk == sequential.
-  * forward: torch float64 re-implementation written independently in the
-    test (full-sequence causal attention, smear recurrence unrolled).
+  * forward (model.OracleModel.step, full.gpt_call): logits written by the
+    reference's own PyTorch port, flaxchat/torch_port/torch_gpt.py
+    GELU_GPT(mlp="relu2"), on the same weights (tests/golden/
+    make_torchport_golden.py, tests/test_torchport_pin.py: within 1e-5;
+    planted mistakes in full.gpt_call are caught); also a torch float64
+    re-implementation written independently in the test.
   * top-k: brute-force sort with explicit tie rule; probs sum to 1.
   * accept step: hand-crafted known-answer cases (full accept, mid reject,
     last-index reject quirk, q == 0 branch, zero residual mass, short round).

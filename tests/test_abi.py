@@ -83,3 +83,17 @@ def test_workspace_size_query_needs_no_gpu():
     nb = _lib.lib().fc_forward_workspace_bytes(ctypes.byref(m), 4, 20, 5, 0)
     assert nb > 20 * 256 * 4 * 3
     assert _lib.lib().fc_attention_workspace_bytes(4, 5, 6, 6, 128, 1024) > 0
+
+
+def test_workspace_sizing_for_narrow_fp32_models():
+    """Workspace sizing is host arithmetic only. An fp32 model narrower than a
+    64-column GEMM tile (n_embd 32) once divided by zero while planning bf16
+    K splits the fp32 path never uses; it must return a size."""
+    L = _lib.lib()
+    layers = (_lib.FcLayer * 2)()
+    lp = ctypes.cast(layers, ctypes.POINTER(_lib.FcLayer))
+    tgt = _lib.FcModel(2, 32, 2, 1, 16, 128, 128, _lib.FC_F32, 1, 1, 1, 0.0, 0.2, 1, 1, 640, lp)
+    drf = _lib.FcModel(1, 32, 2, 1, 16, 128, 128, _lib.FC_F32, 1, 1, 1, 0.0, 0.2, 1, 1, 640, lp)
+    assert L.fc_spec_workspace_bytes(ctypes.byref(tgt), ctypes.byref(drf), 1, 3) > 0
+    for M in (1, 5, 16, 40):
+        assert L.fc_forward_workspace_bytes(ctypes.byref(tgt), 1, M, M, M) > 0
