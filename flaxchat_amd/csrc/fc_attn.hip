@@ -28,6 +28,8 @@
 // the reference's operation order (scores, max, exp, normalise, weighted sum).
 #include "fc_common.h"
 #include "fc_internal.h"
+#include <mutex>
+#include <string>
 
 // K/V cache loads are streamed once per call: non-temporal loads keep them
 // from displacing reusable lines in the caches (measured ~8% faster at cfg4)
@@ -918,4 +920,79 @@ extern "C" int32_t fc_attention(const void* q, const void* kc, const void* vc, v
   FC_CHECK_ARG(max_keys > 0 && max_keys <= cap, "max_keys must be in [1, cap]");
   return fc_launch_attention(q, kc, vc, y, batch, max_tokens, max_per_row, max_per_row, n_head, n_kv_head, head_dim,
                              cap, row_off, start, window, max_keys, dtype, work, work_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// fc_attention_noalloc: fc_attention for callers that cannot allocate (code
+// under stream capture, serving loops that forbid allocation). The split-KV
+// partials (unnormalised O and (max, sum) per query column and key split)
+// live in `scratch`, a file-scope device array each GPU holds until the
+// process ends. Nothing in it has to start at zero: a launch writes every
+// partial its combine step reads (empty key splits write (-inf, 0)). All
+// calls on one GPU share that GPU's array, so calls that overlap in time on
+// one GPU (different streams, or host threads) race; calls ordered on one
+// stream do not.
+// ---------------------------------------------------------------------------
+#ifndef FC_NOALLOC_SCRATCH_BYTES
+#define FC_NOALLOC_SCRATCH_BYTES (32ll << 20)
+#endif
+static __device__ __align__(256) char scratch[FC_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices];  // device address of `scratch`, per device
+}  // namespace
+
+// The device address of `scratch` on the GPU `stream` runs on (the current
+// device for the null stream), looked up once per device with that device
+// current. Host code must use this address, never the array's name.
+static int fc_scratch_ptr(hipStream_t stream, void** out) {
+  int cur = 0;
+  FC_HIP(hipGetDevice(&cur));
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = 0;
+    FC_HIP(hipStreamGetDevice(stream, &sd));
+    dev = (int)sd;
+  }
+  FC_CHECK_ARG(dev >= 0 && dev < kScratchMaxDevices, "device ordinal beyond the scratch table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) FC_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) FC_HIP(hipSetDevice(cur));
+    if (e != hipSuccess || p == nullptr) {
+      fc_set_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return FC_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FC_OK;
+}
+
+extern "C" int64_t fc_attention_noalloc_max_bytes(void) { return FC_NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int32_t fc_attention_noalloc(const void* q, const void* kc, const void* vc, void* y, int32_t batch,
+                                        int32_t max_tokens, int32_t max_per_row, int32_t n_head, int32_t n_kv_head,
+                                        int32_t head_dim, int32_t cap, const int32_t* row_off, const int32_t* start,
+                                        int32_t window, int32_t max_keys, int32_t dtype, void* stream) {
+  FC_CHECK_ARG(q && kc && vc && y && row_off && start, "null pointer");
+  FC_CHECK_ARG(batch > 0 && max_tokens > 0 && max_per_row > 0 && n_head > 0 && n_kv_head > 0, "sizes");
+  FC_CHECK_ARG(max_keys > 0 && max_keys <= cap, "max_keys must be in [1, cap]");
+  const int64_t need = fc_attn_part_bytes(batch, max_per_row, n_head, n_kv_head, head_dim, max_keys);
+  if (need > FC_NOALLOC_SCRATCH_BYTES) {
+    fc_set_error("fc_attention_noalloc: these sizes need " + std::to_string(need) +
+                 " bytes of split-KV partials; the static scratch holds " +
+                 std::to_string((long long)FC_NOALLOC_SCRATCH_BYTES) + " (use fc_attention with a workspace)");
+    return FC_ERR_CAPACITY;
+  }
+  void* part = nullptr;
+  const int rc = fc_scratch_ptr((hipStream_t)stream, &part);
+  if (rc != FC_OK) return rc;
+  return fc_launch_attention(q, kc, vc, y, batch, max_tokens, max_per_row, max_per_row, n_head, n_kv_head, head_dim,
+                             cap, row_off, start, window, max_keys, dtype, part, FC_NOALLOC_SCRATCH_BYTES,
+                             (hipStream_t)stream);
 }

@@ -215,6 +215,22 @@ int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y,
                      const int32_t* start, int32_t window, int32_t max_keys, int32_t dtype, void* work,
                      int64_t work_bytes, void* stream);
 
+/* fc_attention without the workspace argument: the split-KV partials live in
+ * a static device array of the library, fc_attention_noalloc_max_bytes()
+ * bytes (32 MiB), which each GPU the library runs on holds until the process
+ * ends. No counterpart in the reference: for callers that cannot allocate
+ * (code under stream capture, serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and result as fc_attention; sizes whose
+ * partials (fc_attention_workspace_bytes) exceed the array return
+ * FC_ERR_CAPACITY before anything is launched. Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU race. */
+int64_t fc_attention_noalloc_max_bytes(void);
+int32_t fc_attention_noalloc(const void* q, const void* kc, const void* vc, void* y,
+                             int32_t batch, int32_t max_tokens, int32_t max_per_row, int32_t n_head,
+                             int32_t n_kv_head, int32_t head_dim, int32_t cap, const int32_t* row_off,
+                             const int32_t* start, int32_t window, int32_t max_keys, int32_t dtype,
+                             void* stream);
+
 /* Attention prologue of one layer for M packed tokens (flaxchat/engine.py:96-126,
  * flaxchat/gpt.py:52-71; the piece fc_forward runs between the QKV GEMM and the
  * attention). qkv: the QKV GEMM output, fp32 [M][(H + 2G) * head_dim] (q heads,

@@ -43,6 +43,9 @@ def test_argument_errors_are_status_codes():
     assert rc == -1 and b"null" in L.fc_last_error()
     rc = L.fc_attention(None, None, None, None, 1, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None, 0, None)
     assert rc == -1
+    rc = L.fc_attention_noalloc(None, None, None, None, 1, 1, 1, 1, 1, 128, 32, None, None, 0, 1, 1, None)
+    assert rc == -1 and b"null" in L.fc_last_error()
+    assert L.fc_attention_noalloc_max_bytes() == 32 << 20
     st = _lib.FcSpecState()
     assert L.fc_spec_accept(ctypes.byref(st), None) == -1
     m, c = _lib.FcModel(), _lib.FcCache()
