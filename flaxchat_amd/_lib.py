@@ -67,7 +67,7 @@ class FcSpecState(Structure):
 
 EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forward", "fc_gemm", "fc_pack_operand",
            "fc_attention_workspace_bytes", "fc_attention", "fc_attention_noalloc", "fc_attention_noalloc_max_bytes",
-           "fc_attn_prologue", "fc_row_stats", "fc_spec_workspace_bytes",
+           "fc_attn_prologue", "fc_attn_qkv_workspace_bytes", "fc_attn_qkv", "fc_row_stats", "fc_spec_workspace_bytes",
            "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_engine_sample", "fc_cross_entropy",
            "fc_graph_begin", "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
 
@@ -91,6 +91,10 @@ def _declare(L):
     L.fc_attn_prologue.argtypes = [POINTER(FcModel), i32, POINTER(FcCache), vp, vp, vp, vp, vp, i32, vp, vp]
     L.fc_attention.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64,
                                vp]
+    L.fc_attn_qkv_workspace_bytes.argtypes = [POINTER(FcModel), i32, i32]
+    L.fc_attn_qkv_workspace_bytes.restype = i64
+    L.fc_attn_qkv.argtypes = [POINTER(FcModel), i32, POINTER(FcCache), vp, vp, vp, vp, i32, i32, vp, vp, i64, vp]
+    L.fc_attn_qkv.restype = i32
     L.fc_attention_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp]
     L.fc_attention_noalloc.restype = i32
     L.fc_attention_noalloc_max_bytes.argtypes = []

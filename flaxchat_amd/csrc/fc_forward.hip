@@ -56,7 +56,14 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
   const int b = blockIdx.x;
   const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
   const int base = sp.base, n = sp.n, s0 = start[b];
-  if (n <= 0 || s0 < 0) return;
+  if (n <= 0 || s0 < 0) {
+    // a rejected row is empty: its packed slots (clamped to the capacity)
+    // get row -1, which the attention prologue and the fused QKV epilogue
+    // skip, so no stale index from an earlier chunk can write a cache row
+    const int lo = max(row_off[b], 0), hi = min(row_off[b + 1], Mcap);
+    for (int j = lo + (int)threadIdx.x; j < hi; j += blockDim.x) tok_row[j] = -1;
+    return;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int j = threadIdx.x; j < n; j += blockDim.x) {
     tok_row[base + j] = b;
@@ -461,4 +468,62 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     if (rc) return rc;
   }
   return FC_OK;
+}
+
+// QKV projection of one layer with its attention prologue: the fused GEMM
+// epilogue (EPI_QKV) where the plan provides one (bf16, head_dim 128, verify
+// and prefill row counts), else the GEMM into `work` and k_prologue.
+extern "C" int64_t fc_attn_qkv_workspace_bytes(const fc_model* m, int32_t M, int32_t typ_tokens) {
+  if (!m || M <= 0 || m->n_head <= 0 || m->n_kv_head <= 0) return -1;
+  const int hd = m->head_dim, NQKV = (m->n_head + 2 * m->n_kv_head) * hd;
+  if (fc_gemm_fuses_qkv(typ_of(M, typ_tokens), NQKV, m->n_embd, m->dtype, hd)) return 0;
+  return fc_align((int64_t)M * NQKV * 4);
+}
+
+extern "C" int32_t fc_attn_qkv(const fc_model* m, int32_t layer, const fc_cache* c, const void* h,
+                               const int32_t* tokens, const int32_t* tok_row, const int32_t* tok_pos, int32_t M,
+                               int32_t typ_tokens, void* q, void* work, int64_t work_bytes, void* stream) {
+  int rc = check_model(m);
+  if (rc) return rc;
+  FC_CHECK_ARG(c && c->k && c->v && c->batch > 0 && c->cap > 0 && c->cap % 32 == 0, "cache");
+  FC_CHECK_ARG(h && tokens && tok_row && tok_pos && q, "null pointer");
+  FC_CHECK_ARG(layer >= 0 && layer < m->n_layer, "layer out of range");
+  FC_CHECK_ARG(M >= 0, "M");
+  if (M == 0) return FC_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int D = m->n_embd, H = m->n_head, G = m->n_kv_head, hd = m->head_dim;
+  const int NQKV = (H + 2 * G) * hd, Mtyp = typ_of(M, typ_tokens);
+  const fc_layer& L = m->layers[layer];
+  const int64_t need = fc_attn_qkv_workspace_bytes(m, M, typ_tokens);
+  FC_CHECK_ARG(need == 0 || (work && work_bytes >= need), "fc_attn_qkv workspace too small");
+  Epi e{};
+  if (need == 0) {
+    e.mode = EPI_QKV;
+    QkvEpi& Q = e.qkv;
+    Q.tokens = tokens;
+    Q.tok_row = tok_row;
+    Q.tok_pos = tok_pos;
+    Q.rcos = m->rope_cos;
+    Q.rsin = m->rope_sin;
+    Q.rope_len = m->rope_len;
+    Q.ve = (const uint16_t*)L.ve;
+    Q.ve_gate = L.ve_gate;
+    Q.h = (const uint16_t*)h;
+    Q.D = D;
+    Q.H = H;
+    Q.G = G;
+    Q.B = c->batch;
+    Q.cap = c->cap;
+    const int64_t layer_elems = (int64_t)c->batch * G * c->cap * hd;
+    Q.kc = (uint16_t*)c->k + layer_elems * layer;
+    Q.vc = (uint16_t*)c->v + layer_elems * layer;
+    Q.q = (uint16_t*)q;
+    return fc_launch_gemm(h, L.wqkv, M, nullptr, Mtyp, NQKV, D, m->dtype, e, GemmWork{}, s, nullptr);
+  }
+  e.mode = EPI_STORE;
+  e.out = work;
+  e.ldo = NQKV;
+  rc = fc_launch_gemm(h, L.wqkv, M, nullptr, Mtyp, NQKV, D, m->dtype, e, GemmWork{}, s, nullptr);
+  if (rc) return rc;
+  return fc_launch_prologue((const float*)work, h, tokens, m, layer, c, tok_row, tok_pos, M, nullptr, q, s);
 }

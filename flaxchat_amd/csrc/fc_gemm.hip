@@ -443,7 +443,10 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
     x2[0] = b0.x; x2[1] = b0.y; x2[2] = b0.z; x2[3] = b0.w; x2[4] = b1.x; x2[5] = b1.y; x2[6] = b1.z; x2[7] = b1.w;
   }
   const int b = p.b, pos = p.pos;
-  const bool in_cache = live && (unsigned)b < (unsigned)Q.B && pos >= 0 && pos < Q.cap;
+  // a token whose row lies outside [0, B) (an empty or rejected chunk row)
+  // writes nothing, q included, like the unfused prologue
+  const bool in_row = live && (unsigned)b < (unsigned)Q.B;
+  const bool in_cache = in_row && pos >= 0 && pos < Q.cap;
   if (hh < Q.H + Q.G) {
     float ss = 0.f;
 #pragma unroll
@@ -468,7 +471,7 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
       w2[e] = (uint32_t)f2bf(x2[2 * e] * inv * 1.2f) | ((uint32_t)f2bf(x2[2 * e + 1] * inv * 1.2f) << 16);
     }
     if (hh < Q.H) {
-      if (live) {
+      if (in_row) {
         bf16_t* qo = Q.q + ((int64_t)m * Q.H + hh) * 128;
         *(uint4*)(qo + 8 * part) = p1;
         *(uint4*)(qo + 64 + 8 * part) = p2;

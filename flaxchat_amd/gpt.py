@@ -12,6 +12,8 @@ GEMMs stream. Arrays are numpy float32 on the host.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 from typing import Dict, List, Optional
 
@@ -151,6 +153,62 @@ class GPT:
             blocks.append(Block(attn, mlp))
         value_embeds = {str(i): Embed(nrm(Vp, G * d)) for i in range(L) if has_ve(i, L)}
         smear_gate = Linear(nrm(24, 1))
+        resid, x0 = reference_lambdas(L)
+        return cls(config, wte, blocks, lm_head, resid, x0, smear_gate,
+                   np.zeros(1, np.float32), np.full(1, 0.2, np.float32), value_embeds)
+
+    @classmethod
+    def init_normal_parallel(cls, config: GPTConfig, seed: int = 0, std: float = 0.02,
+                             threads: Optional[int] = None) -> "GPT":
+        """init_normal's recipe (same tensors, same draw order, N(0, std),
+        reference scalars) with each tensor drawn from its own stream, so
+        the draws run in threads: tensor i of the draw order takes child i
+        of SeedSequence(seed), split into row blocks of about 4M elements
+        that take that child's children in order. Same distribution as
+        init_normal, different values; for the large configurations (a d24
+        model at vocabulary 65536 holds about 2.1e9 parameters)."""
+        from concurrent.futures import ThreadPoolExecutor
+        D, H, G, L = config.n_embd, config.n_head, config.n_kv_head, config.n_layer
+        d = D // H
+        Vp = padded_vocab(config)
+        shapes = [(Vp, D)]
+        if not config.tie_embeddings:
+            shapes.append((D, Vp))
+        for i in range(L):
+            shapes += [(D, H * d), (D, G * d), (D, G * d), (D, D), (D, 4 * D), (4 * D, D)]
+            if has_ve(i, L):
+                shapes.append((12, G))
+        shapes += [(Vp, G * d) for i in range(L) if has_ve(i, L)]
+        shapes.append((24, 1))
+        out = [np.empty(s, np.float32) for s in shapes]
+        jobs = []
+        for t, child in enumerate(np.random.SeedSequence(seed).spawn(len(shapes))):
+            rows, cols = shapes[t]
+            per = max(1, (1 << 22) // cols)
+            nblk = (rows + per - 1) // per
+            for j, ss in enumerate(child.spawn(nblk)):
+                jobs.append((t, j * per, min(rows, (j + 1) * per), ss))
+
+        def draw(job):
+            t, r0, r1, ss = job
+            blk = out[t][r0:r1]
+            np.random.Generator(np.random.PCG64(ss)).standard_normal(blk.shape, dtype=np.float32, out=blk)
+            blk *= np.float32(std)
+
+        with ThreadPoolExecutor(max_workers=threads or min(16, os.cpu_count() or 1)) as ex:
+            list(ex.map(draw, jobs))
+        it = iter(out)
+        wte = Embed(next(it))
+        lm_head = None if config.tie_embeddings else Linear(next(it))
+        blocks = []
+        for i in range(L):
+            attn = Attention(Linear(next(it)), Linear(next(it)), Linear(next(it)), Linear(next(it)))
+            mlp = MLP(Linear(next(it)), Linear(next(it)))
+            if has_ve(i, L):
+                attn.ve_gate = Linear(next(it))
+            blocks.append(Block(attn, mlp))
+        value_embeds = {str(i): Embed(next(it)) for i in range(L) if has_ve(i, L)}
+        smear_gate = Linear(next(it))
         resid, x0 = reference_lambdas(L)
         return cls(config, wte, blocks, lm_head, resid, x0, smear_gate,
                    np.zeros(1, np.float32), np.full(1, 0.2, np.float32), value_embeds)

@@ -16,6 +16,28 @@ Operators:
                                      (flaxchat/engine.py:128-156)
   cross_entropy(logits, targets)     per-row logsumexp(z) - z[t], 0 where t < 0
                                      (flaxchat/gpt.py:446-452)
+
+The engine entry points take a model as the address of its fc_model
+descriptor (`DeviceModel.desc`, read-only weights that stay alive with the
+DeviceModel) and everything they write as tensors, declared mutated:
+  forward(model, k_cache, v_cache, hist, tokens, row_off, start, max_per_row, n_out, logits,
+          workspace, typ_tokens=0, flags=0)
+                                     one packed chunk through the model (fc_forward;
+                                     flaxchat/engine.py:51-177, 396-407)
+  attn_prologue(model, layer, k_cache, v_cache, qkv, h, tokens, tok_row, tok_pos) -> q
+                                     RoPE, QK-norm, VE gate, cache append (engine.py:96-126)
+  attn_qkv(model, layer, k_cache, v_cache, h, tokens, tok_row, tok_pos, typ_tokens=0) -> q
+                                     the QKV projection with that prologue fused
+  row_stats(logits, temperature, top_k) -> (mx, sum, tau, tie_idx, argmax)
+                                     top-k keep set and softmax statistics (engine.py:461-476)
+  spec_accept(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed)
+                                     accept / reject / bonus and the rollback bookkeeping
+                                     (engine.py:525-606) on a round's logits
+  spec_round(target, draft, t_k, t_v, t_hist, d_k, d_v, d_hist, buffers, batch, k, max_tokens,
+             gen_cap, vocab, temperature, top_k, seed, workspace)
+                                     one whole speculative round (engine.py:484-606)
+`buffers` is the speculative state's device arrays in fc_spec_state order
+(`SPEC_BUFFERS`: t_len .. p_stats, then the partials buffer `part`).
 """
 
 from __future__ import annotations
@@ -25,7 +47,8 @@ import torch
 from . import _lib
 from ._lib import check, lib
 
-__all__ = ["pack_operand", "linear", "attention", "cross_entropy", "frag_to_rows"]
+__all__ = ["pack_operand", "linear", "attention", "cross_entropy", "frag_to_rows", "forward", "attn_prologue",
+           "attn_qkv", "row_stats", "spec_accept", "spec_round", "SPEC_BUFFERS"]
 
 NS = "flaxchat_mi355x"
 
@@ -156,3 +179,182 @@ def cross_entropy(logits: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
 @cross_entropy.register_fake
 def _(logits, targets):
     return logits.new_empty((logits.shape[0],))
+
+
+# ---------------------------------------------------------------- engine entry points
+import ctypes  # noqa: E402
+from typing import List, Tuple  # noqa: E402
+
+SPEC_BUFFERS = list(_lib._SPEC_PTRS) + ["part"]
+
+
+def _model(addr: int) -> "ctypes.pointer":
+    if addr == 0:
+        raise ValueError("model: the address of an fc_model descriptor (DeviceModel.desc)")
+    return ctypes.cast(ctypes.c_void_p(addr), ctypes.POINTER(_lib.FcModel))
+
+
+def _cache(k_cache: torch.Tensor, v_cache: torch.Tensor, hist: torch.Tensor = None) -> _lib.FcCache:
+    """fc_cache over one model's cache tensors: k [L][B][G][cap][hd],
+    v of as many elements, hist [B][cap][n_embd] fp32 (or absent)."""
+    if k_cache.dim() != 5 or v_cache.numel() != k_cache.numel():
+        raise ValueError("k_cache [layers][batch][kv heads][cap][head_dim] and a v_cache of as many elements")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("the caches must be contiguous")
+    B, cap = k_cache.shape[1], k_cache.shape[3]
+    if hist is not None and (hist.dtype != torch.float32 or hist.shape[:2] != (B, cap) or not hist.is_contiguous()):
+        raise ValueError("hist: contiguous fp32 [batch][cap][n_embd]")
+    return _lib.FcCache(k_cache.data_ptr(), v_cache.data_ptr(), hist.data_ptr() if hist is not None else 0, B, cap)
+
+
+def _i32(*ts):
+    for t in ts:
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError("index arrays are contiguous int32 tensors")
+
+
+@torch.library.custom_op(f"{NS}::forward", mutates_args=("k_cache", "v_cache", "hist", "logits", "workspace"))
+def forward(model: int, k_cache: torch.Tensor, v_cache: torch.Tensor, hist: torch.Tensor, tokens: torch.Tensor,
+            row_off: torch.Tensor, start: torch.Tensor, max_per_row: int, n_out: int, logits: torch.Tensor,
+            workspace: torch.Tensor, typ_tokens: int = 0, flags: int = 0) -> None:
+    m = _model(model)
+    c = _cache(k_cache, v_cache, hist)
+    _i32(tokens, row_off, start)
+    B = c.batch
+    if row_off.numel() != B + 1 or start.numel() != B:
+        raise ValueError("forward: row_off has batch + 1 entries and start batch")
+    V = m.contents.vocab
+    if n_out > 0 and (logits.dtype != torch.float32 or logits.numel() < B * n_out * V or not logits.is_contiguous()):
+        raise ValueError("forward: logits is contiguous fp32 with at least batch * n_out * vocab elements")
+    need = lib().fc_forward_workspace_bytes(m, B, tokens.numel(), max_per_row, typ_tokens)
+    if need < 0 or workspace.numel() < need:
+        raise ValueError(f"forward: workspace of {workspace.numel()} bytes, {need} needed")
+    ch = _lib.FcChunk(tokens.numel(), max_per_row, typ_tokens, tokens.data_ptr(), row_off.data_ptr(),
+                      start.data_ptr(), n_out, logits.data_ptr() if n_out > 0 else 0, n_out * V, flags)
+    check(lib().fc_forward(m, ctypes.byref(c), ctypes.byref(ch), workspace.data_ptr(), workspace.numel(),
+                           _stream(tokens)), "fc_forward")
+
+
+@forward.register_fake
+def _(model, k_cache, v_cache, hist, tokens, row_off, start, max_per_row, n_out, logits, workspace, typ_tokens=0,
+      flags=0):
+    return None
+
+
+def _q_out(model: int, M: int, like: torch.Tensor) -> torch.Tensor:
+    m = _model(model).contents
+    dt = torch.bfloat16 if m.dtype == _lib.FC_BF16 else torch.float32
+    return torch.empty((M, m.n_head, m.head_dim), dtype=dt, device=like.device)
+
+
+@torch.library.custom_op(f"{NS}::attn_prologue", mutates_args=("k_cache", "v_cache"))
+def attn_prologue(model: int, layer: int, k_cache: torch.Tensor, v_cache: torch.Tensor, qkv: torch.Tensor,
+                  h: torch.Tensor, tokens: torch.Tensor, tok_row: torch.Tensor, tok_pos: torch.Tensor) -> torch.Tensor:
+    _i32(tokens, tok_row, tok_pos)
+    M = tokens.numel()
+    if qkv.dtype != torch.float32 or qkv.dim() != 2 or qkv.shape[0] < M or not qkv.is_contiguous():
+        raise ValueError("attn_prologue: qkv is contiguous fp32 [M][(H + 2G) * head_dim]")
+    c = _cache(k_cache, v_cache)
+    q = _q_out(model, M, qkv)
+    check(lib().fc_attn_prologue(_model(model), layer, ctypes.byref(c), qkv.data_ptr(), h.data_ptr(),
+                                 tokens.data_ptr(), tok_row.data_ptr(), tok_pos.data_ptr(), M, q.data_ptr(),
+                                 _stream(qkv)), "fc_attn_prologue")
+    return q
+
+
+def _q_fake(model: int, M, like: torch.Tensor, cache: torch.Tensor) -> torch.Tensor:
+    m = _model(model).contents  # the descriptor is host memory: readable while tracing
+    return like.new_empty((M, m.n_head, m.head_dim), dtype=cache.dtype)
+
+
+@attn_prologue.register_fake
+def _(model, layer, k_cache, v_cache, qkv, h, tokens, tok_row, tok_pos):
+    return _q_fake(model, tokens.shape[0], qkv, k_cache)
+
+
+@torch.library.custom_op(f"{NS}::attn_qkv", mutates_args=("k_cache", "v_cache"))
+def attn_qkv(model: int, layer: int, k_cache: torch.Tensor, v_cache: torch.Tensor, h: torch.Tensor,
+             tokens: torch.Tensor, tok_row: torch.Tensor, tok_pos: torch.Tensor, typ_tokens: int = 0) -> torch.Tensor:
+    _i32(tokens, tok_row, tok_pos)
+    M = tokens.numel()
+    m = _model(model)
+    c = _cache(k_cache, v_cache)
+    q = _q_out(model, M, h)
+    need = lib().fc_attn_qkv_workspace_bytes(m, M, typ_tokens)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=h.device)
+    check(lib().fc_attn_qkv(m, layer, ctypes.byref(c), h.data_ptr(), tokens.data_ptr(), tok_row.data_ptr(),
+                            tok_pos.data_ptr(), M, typ_tokens, q.data_ptr(), ws.data_ptr(), ws.numel(), _stream(h)),
+          "fc_attn_qkv")
+    return q
+
+
+@attn_qkv.register_fake
+def _(model, layer, k_cache, v_cache, h, tokens, tok_row, tok_pos, typ_tokens=0):
+    return _q_fake(model, tokens.shape[0], h, k_cache)
+
+
+@torch.library.custom_op(f"{NS}::row_stats", mutates_args=())
+def row_stats(logits: torch.Tensor, temperature: float, top_k: int) -> Tuple[torch.Tensor, torch.Tensor,
+                                                                             torch.Tensor, torch.Tensor,
+                                                                             torch.Tensor]:
+    if logits.dtype != torch.float32 or logits.dim() != 2 or not logits.is_contiguous():
+        raise ValueError("row_stats takes contiguous fp32 logits [rows][V]")
+    rows, V = logits.shape
+    raw = torch.empty((rows, 8), dtype=torch.int32, device=logits.device)
+    check(lib().fc_row_stats(logits.data_ptr(), rows, V, temperature, top_k, raw.data_ptr(), _stream(logits)),
+          "fc_row_stats")
+    f = raw.view(torch.float32)
+    return f[:, 0].clone(), f[:, 1].clone(), f[:, 2].clone(), raw[:, 3].clone(), raw[:, 4].clone()
+
+
+@row_stats.register_fake
+def _(logits, temperature, top_k):
+    r = logits.shape[0]
+    f = lambda: logits.new_empty((r,))  # noqa: E731
+    i = lambda: logits.new_empty((r,), dtype=torch.int32)  # noqa: E731
+    return f(), f(), f(), i(), i()
+
+
+def _spec_state(buffers: List[torch.Tensor], batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed):
+    if len(buffers) != len(SPEC_BUFFERS):
+        raise ValueError(f"buffers: the {len(SPEC_BUFFERS)} arrays of SPEC_BUFFERS in order")
+    for name, t in zip(SPEC_BUFFERS, buffers):
+        if not t.is_contiguous():
+            raise ValueError(f"buffer {name} must be contiguous")
+    part = buffers[-1]
+    return _lib.FcSpecState(batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed,
+                            *[t.data_ptr() for t in buffers[:-1]], part.data_ptr(), part.numel())
+
+
+@torch.library.custom_op(f"{NS}::spec_accept", mutates_args=("buffers",))
+def spec_accept(buffers: List[torch.Tensor], batch: int, k: int, max_tokens: int, gen_cap: int, vocab: int,
+                temperature: float, top_k: int, seed: int) -> None:
+    st = _spec_state(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed)
+    check(lib().fc_spec_accept(ctypes.byref(st), _stream(buffers[0])), "fc_spec_accept")
+
+
+@spec_accept.register_fake
+def _(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed):
+    return None
+
+
+@torch.library.custom_op(f"{NS}::spec_round",
+                         mutates_args=("t_k", "t_v", "t_hist", "d_k", "d_v", "d_hist", "buffers", "workspace"))
+def spec_round(target: int, draft: int, t_k: torch.Tensor, t_v: torch.Tensor, t_hist: torch.Tensor,
+               d_k: torch.Tensor, d_v: torch.Tensor, d_hist: torch.Tensor, buffers: List[torch.Tensor], batch: int,
+               k: int, max_tokens: int, gen_cap: int, vocab: int, temperature: float, top_k: int, seed: int,
+               workspace: torch.Tensor) -> None:
+    mt, md = _model(target), _model(draft)
+    tc, dc = _cache(t_k, t_v, t_hist), _cache(d_k, d_v, d_hist)
+    st = _spec_state(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed)
+    need = lib().fc_spec_workspace_bytes(mt, md, batch, k)
+    if need < 0 or workspace.numel() < need:
+        raise ValueError(f"spec_round: workspace of {workspace.numel()} bytes, {need} needed")
+    check(lib().fc_spec_round(mt, ctypes.byref(tc), md, ctypes.byref(dc), ctypes.byref(st), workspace.data_ptr(),
+                              workspace.numel(), _stream(workspace)), "fc_spec_round")
+
+
+@spec_round.register_fake
+def _(target, draft, t_k, t_v, t_hist, d_k, d_v, d_hist, buffers, batch, k, max_tokens, gen_cap, vocab, temperature,
+      top_k, seed, workspace):
+    return None

@@ -245,6 +245,19 @@ int32_t fc_attn_prologue(const fc_model* m, int32_t layer, const fc_cache* c, co
                          const void* h, const int32_t* tokens, const int32_t* tok_row,
                          const int32_t* tok_pos, int32_t M, void* q, void* stream);
 
+/* QKV projection of one layer followed by its attention prologue
+ * (flaxchat/engine.py:96-126: the c_q / c_k / c_v matmuls of :106-108, then
+ * what fc_attn_prologue does) for M tokens: h is the normalised input (bf16:
+ * fragment order over round16(M) rows; fp32: row-major [M][n_embd]); q, the
+ * cache writes and the skipped tokens as in fc_attn_prologue. For bf16,
+ * head_dim 128 and verify / prefill row counts (typ_tokens, 0 = M) the
+ * prologue runs in the GEMM's epilogue and no workspace is used; otherwise
+ * the fp32 projection goes to `work` (fc_attn_qkv_workspace_bytes). */
+int64_t fc_attn_qkv_workspace_bytes(const fc_model* m, int32_t M, int32_t typ_tokens);
+int32_t fc_attn_qkv(const fc_model* m, int32_t layer, const fc_cache* c, const void* h,
+                    const int32_t* tokens, const int32_t* tok_row, const int32_t* tok_pos, int32_t M,
+                    int32_t typ_tokens, void* q, void* work, int64_t work_bytes, void* stream);
+
 /* Per-row statistics of fp32 logits rows (flaxchat/engine.py:461-476):
  * lax.top_k keep-set (exactly k, lower index first among ties), max and
  * softmax normaliser of z/T over it, and the first-index argmax. */

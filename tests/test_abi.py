@@ -51,6 +51,7 @@ def test_argument_errors_are_status_codes():
     m, c = _lib.FcModel(), _lib.FcCache()
     assert L.fc_attn_prologue(ctypes.byref(m), 0, ctypes.byref(c), None, None, None, None, None, 1, None, None) == -1
     assert b"null" in L.fc_last_error()
+    assert L.fc_attn_qkv(ctypes.byref(m), 0, ctypes.byref(c), None, None, None, None, 1, 0, None, None, 0, None) == -1
 
 
 def test_struct_layout_matches_c(tmp_path):

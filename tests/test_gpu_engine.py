@@ -3,7 +3,8 @@
 fp32 (parity mode): logits within 1e-3 max-abs of the oracle (the north-star
 tolerance; observed ~1e-5) and token streams identical under greedy and
 under sampling (same Philox stream; a flip would need two candidates within
-fp32 rounding). bf16: logits within 5e-2 max-abs of the fp32 oracle.
+fp32 rounding). bf16: logits within 1e-2 max-abs of the fp32 oracle at the
+cfg1 width (measured ~5e-3; bounds are about twice the printed errors).
 """
 
 import ctypes
@@ -74,7 +75,9 @@ def test_forward_logits_vs_oracle(which, dtype, tiny_pair, cfg1_pair):
         got3 = _device_logits(tgt, toks3, dtype, [130, 10])
         err = max(err, np.abs(got3 - ref3).max())
     _say(f"  max abs err {err:.3e}")
-    assert err < (1e-3 if dtype == "fp32" else 5e-2)
+    # bf16 bounds about twice the measured error (tiny: head_dim 32 and
+    # N(0, 0.1) weights give larger logits; measured 1.6e-2 and 4.8e-3)
+    assert err < (1e-3 if dtype == "fp32" else (3e-2 if which == "tiny" else 1e-2))
 
 
 def test_single_token_rows_bf16(cfg1_pair):
@@ -101,7 +104,7 @@ def test_single_token_rows_bf16(cfg1_pair):
         ref = _oracle_logits(tgt, prompts[b] + nxt[b])[len(prompts[b]):]
         err = max(err, np.abs(np.stack([g[b] for g in got]) - ref).max())
     _say(f"single-token rows bf16: max abs err {err:.3e}")
-    assert err < 5e-2
+    assert err < 1e-2
 
 
 def test_prefill_size_chunk_bf16(cfg1_pair):
@@ -125,15 +128,24 @@ def test_prefill_size_chunk_bf16(cfg1_pair):
     forward_rows(dm, small, [r[-1:] for r in rows], [len(r) - 1 for r in rows], 1, lg_small, ws)
     torch.cuda.synchronize()
     a, b = lg_big.cpu().numpy()[:, 0], lg_small.cpu().numpy()[:, 0]
+    e_ref = e_ab = 0.0
     for i, r in enumerate(rows):
         ref = _oracle_logits(tgt, r)[-1]
-        assert np.abs(a[i] - ref).max() < 5e-2, (i, np.abs(a[i] - ref).max())
-        assert np.abs(a[i] - b[i]).max() < 5e-2, (i, np.abs(a[i] - b[i]).max())
-    # the K / V cache written by both paths
+        e_ref = max(e_ref, float(np.abs(a[i] - ref).max()))
+        e_ab = max(e_ab, float(np.abs(a[i] - b[i]).max()))
+    _say(f"prefill-size chunk: logits vs oracle {e_ref:.3e}, vs small chunks {e_ab:.3e}")
+    assert e_ref < 2e-2 and e_ab < 2e-2
+    # the K / V cache written by both paths (K: the 256 x 256 GEMM's fused
+    # prologue vs the 32 x 128 tile's; V blocks of 32 positions per head)
+    kerr = verr = 0.0
     for i, r in enumerate(rows):
         n = len(r)
-        kb, ks = big.k[:, i, :, :n].float(), small.k[:, i, :, :n].float()
-        assert (kb - ks).abs().max().item() < 5e-2
+        kb, ks = big.k[:, i].float(), small.k[:, i].float()
+        kerr = max(kerr, (kb - ks).abs().max().item())
+        vb, vs = big.v[:, i].float(), small.v[:, i].float()
+        verr = max(verr, (vb - vs).abs().max().item())
+    _say(f"prefill-size chunk: K cache max diff {kerr:.3e}, V cache max diff {verr:.3e}")
+    assert kerr < 5e-2 and verr < 5e-2
 
 
 def test_chunk_equals_steps(cfg1_pair):
@@ -330,3 +342,34 @@ def test_golden_cfg1_streams(case_idx):
     got = generate_speculative(tgt, draft, g["prompt"], max_tokens=64, temperature=c["temperature"],
                                top_k=c["top_k"], seed=c["seed"], draft_steps=c["draft_steps"], dtype="fp32")
     assert got == c["tokens"]
+
+
+def test_rejected_row_writes_no_cache(tiny_pair):
+    """A chunk row with more tokens than max_per_row is treated as empty
+    (include/flaxchat_amd.h): its packed slots must not reuse the row /
+    position indices an earlier chunk left in the same workspace, so no
+    other row's cache is written. fp32: the caches must equal those of the
+    same chunk with that row given no tokens, bit for bit."""
+    from flaxchat_amd.runtime import forward_packed
+    tgt = tiny_pair[0]
+    dm = as_device_model(tgt, "fp32")
+    dev = dm.device
+    i32 = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)  # noqa: E731
+    rng = np.random.default_rng(12)
+    first = [rng.integers(0, 256, n).tolist() for n in (5, 6, 4)]
+    second = [rng.integers(0, 256, n).tolist() for n in (3, 8, 2)]
+    caches = []
+    for drop_row in (False, True):
+        cache = DeviceCache(dm, 3, 64)
+        ws = Workspace(dev)
+        tok = sum(first, [])
+        forward_packed(dm, cache, i32(tok + [0] * 8), i32([0, 5, 11, 15]), i32([0, 0, 0]), 6, 0, None, ws)
+        if drop_row:   # row 1 feeds nothing
+            tok2, off2 = second[0] + second[2], [0, 3, 3, 5]
+        else:          # row 1 feeds 8 > max_per_row tokens: rejected
+            tok2, off2 = second[0] + second[1] + second[2], [0, 3, 11, 13]
+        forward_packed(dm, cache, i32(tok2 + [0] * (23 - len(tok2))), i32(off2), i32([5, 6, 4]), 6, 0, None, ws)
+        torch.cuda.synchronize()
+        caches.append((cache.k.cpu(), cache.v.cpu(), cache.hist.cpu()))
+    for a, b, name in zip(caches[0], caches[1], ("k", "v", "hist")):
+        assert torch.equal(a, b), f"{name} cache differs: the rejected row wrote into another row"

@@ -1,7 +1,8 @@
 """GPT.__call__ on the HIP engine (flaxchat_amd.engine.gpt_forward) against
 the oracle's full-sequence forward (oracle/full.py). Tolerances as the rest
 of the suite: fp32 logits within 1e-3 max-abs,
-bf16 within 5e-2; the loss within 1e-4 relative in fp32."""
+bf16 within 2e-2 (measured errors are printed; about 5e-3 at these
+widths); the loss within 1e-4 relative in fp32."""
 
 import sys
 
@@ -64,7 +65,9 @@ def test_full_forward_bf16_prefill_kernels(cfg1_pair):
     ids = np.random.default_rng(10).integers(0, m.config.vocab_size, (4, 300))
     got = gpt_forward(m, ids, dtype="bf16").cpu().numpy()
     ref = gpt_call(m, ids)
-    assert np.abs(got - ref).max() < 5e-2
+    err = float(np.abs(got - ref).max())
+    _say(f"  max abs err {err:.3e}")
+    assert err < 2e-2
 
 
 def test_full_forward_bf16_big_tiles():
@@ -79,7 +82,9 @@ def test_full_forward_bf16_big_tiles():
     ids = np.random.default_rng(12).integers(0, cfg.vocab_size, (4, 900))
     got = gpt_forward(m, ids, dtype="bf16").cpu().numpy()
     ref = gpt_call(m, ids)
-    assert np.abs(got - ref).max() < 5e-2
+    err = float(np.abs(got - ref).max())
+    _say(f"  max abs err {err:.3e}")
+    assert err < 2e-2
 
 
 def test_full_forward_loss(tiny_pair):
@@ -119,4 +124,6 @@ def test_full_forward_bf16_verify_size_split():
     ids = np.random.default_rng(13).integers(0, cfg.vocab_size, (8, 25))
     got = gpt_forward(m, ids, dtype="bf16").cpu().numpy()
     ref = gpt_call(m, ids)
-    assert np.abs(got - ref).max() < 5e-2
+    err = float(np.abs(got - ref).max())
+    _say(f"  max abs err {err:.3e}")
+    assert err < 2e-2

@@ -262,24 +262,13 @@ def test_row_stats(V, top_k, T):
 
 
 # ---------------------------------------------------------------- accept at full vocabulary
-@pytest.mark.parametrize("T", [1.0, 0.0])
-def test_spec_accept_cfg3_vs_oracle(T):
-    """fc_spec_accept on the config-3 sampling shape (64 rows, k = 4, V =
-    65536: the vocab-wide passes run in 64 chunks per row and merge their
-    partials) against the oracle's accept_round (flaxchat/engine.py:525-592)
-    on the same logits, drafts and Philox counters. Target logits are
-    15 tanh(N(0, 2^2) / 15), the draft's the target's plus N(0, 0.5^2)
-    noise (softcapped again); drafts are the oracle's own draws from the
-    draft logits. The emitted tokens must match exactly."""
-    from oracle import sampling as S
-    _say(f"spec accept cfg3 T={T}")
-    B, k, V, seed = 64, 4, 65536, 1234
-    rng = np.random.default_rng(11)
-    P = (15 * np.tanh(rng.standard_normal((B, k + 1, V)) * 2 / 15)).astype(np.float32)
-    Q = (15 * np.tanh((P[:, :k] + rng.standard_normal((B, k, V)) * 0.5) / 15)).astype(np.float32)
-    rnd = (np.arange(B) % 5).astype(np.int32)
-    drafts = np.array([[S.draft_sample(Q[b, i], T, None, seed, b, int(rnd[b]), i) for i in range(k)]
-                       for b in range(B)], np.int32)
+def _run_accept(P, Q, drafts, rnd, T, top_k, seed):
+    """fc_spec_accept on host-made logits / drafts (the state of a round
+    whose rows each fed one pending token at position 10); the draft's row
+    statistics from fc_row_stats with the round's top-k. Returns the
+    device's result rows and the final round counters."""
+    B, k1, V = P.shape
+    k = k1 - 1
     i32 = dict(dtype=torch.int32, device=dev())
     z = lambda *s: torch.zeros(*s, **i32)  # noqa: E731
     gen_cap, P_MAX = 64, _lib.PMAX
@@ -294,25 +283,109 @@ def test_spec_accept_cfg3_vs_oracle(T):
                 q_stats=torch.zeros(B * k * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev()),
                 p_stats=torch.zeros(B * (k + 1) * ctypes.sizeof(FcRowstat), dtype=torch.uint8, device=dev()),
                 part=torch.zeros(lib().fc_spec_part_bytes(B, k, V), dtype=torch.uint8, device=dev()))
-    st = _lib.FcSpecState(B, k, 40, gen_cap, V, T, 0, seed, *[bufs[n].data_ptr() for n in _lib._SPEC_PTRS],
+    st = _lib.FcSpecState(B, k, 40, gen_cap, V, T, top_k or 0, seed, *[bufs[n].data_ptr() for n in _lib._SPEC_PTRS],
                           bufs["part"].data_ptr(), bufs["part"].numel())
-    # the draft's row statistics come from the draft steps in a round; here from fc_row_stats
-    check(lib().fc_row_stats(bufs["q_logits"].data_ptr(), B * k, V, T, 0, bufs["q_stats"].data_ptr(), stream()),
-          "row stats")
+    check(lib().fc_row_stats(bufs["q_logits"].data_ptr(), B * k, V, T, top_k or 0, bufs["q_stats"].data_ptr(),
+                             stream()), "row stats")
     check(lib().fc_spec_accept(ctypes.byref(st), stream()), "spec accept")
     torch.cuda.synchronize()
-    res = bufs["result"].cpu().numpy()
-    assert np.array_equal(bufs["round"].cpu().numpy(), rnd + 1)
-    n_acc = n_bonus = 0
-    for b in range(B):
-        em, acc, rej, bonus = S.accept_round(P[b], Q[b], drafts[b], T, None, seed, b, int(rnd[b]))
+    return bufs["result"].cpu().numpy(), bufs["round"].cpu().numpy()
+
+
+def _check_accept(P, Q, drafts, rnd, T, top_k, seed):
+    from oracle import sampling as S
+    res, rnd_after = _run_accept(P, Q, drafts, rnd, T, top_k, seed)
+    assert np.array_equal(rnd_after, rnd + 1)
+    recs = []
+    for b in range(P.shape[0]):
+        em, acc, rej, bonus = S.accept_round(P[b], Q[b], drafts[b], T, top_k, seed, b, int(rnd[b]))
         n = int(res[b, 0])
         assert res[b, 8:8 + n].tolist() == em, f"row {b}: {res[b, 8:8 + n].tolist()} vs oracle {em}"
         assert (int(res[b, 1]), int(res[b, 2])) == (acc, rej), f"row {b}"
-        n_acc += acc
-        n_bonus += bonus
+        recs.append((em, acc, rej, bonus))
+    return recs
+
+
+def _cfg3_logits(B, k, V, seed_np=11):
+    rng = np.random.default_rng(seed_np)
+    P = (15 * np.tanh(rng.standard_normal((B, k + 1, V)) * 2 / 15)).astype(np.float32)
+    Q = (15 * np.tanh((P[:, :k] + rng.standard_normal((B, k, V)) * 0.5) / 15)).astype(np.float32)
+    return P, Q
+
+
+@pytest.mark.parametrize("T,top_k", [(1.0, None), (0.0, None), (0.8, 40), (0.0, 40)])
+def test_spec_accept_cfg3_vs_oracle(T, top_k):
+    """fc_spec_accept on the config-3 sampling shape (64 rows, k = 4, V =
+    65536) against the oracle's accept_round (flaxchat/engine.py:525-592) on
+    the same logits, drafts and Philox counters. Without top-k the
+    vocab-wide passes run in 64 chunks per row and merge their partials;
+    with top_k 40 (generate_speculative's default, engine.py:411, 461-466)
+    one workgroup per row finds the keep set by radix select. Target logits
+    are 15 tanh(N(0, 2^2) / 15), the draft's the target's plus N(0, 0.5^2)
+    noise (softcapped again); drafts are the oracle's own draws from the
+    draft logits. The emitted tokens must match exactly."""
+    from oracle import sampling as S
+    _say(f"spec accept cfg3 T={T} top_k={top_k}")
+    B, k, V, seed = 64, 4, 65536, 1234
+    P, Q = _cfg3_logits(B, k, V)
+    rnd = (np.arange(B) % 5).astype(np.int32)
+    drafts = np.array([[S.draft_sample(Q[b, i], T, top_k, seed, b, int(rnd[b]), i) for i in range(k)]
+                       for b in range(B)], np.int32)
+    recs = _check_accept(P, Q, drafts, rnd, T, top_k, seed)
+    n_acc = sum(r[1] for r in recs)
+    n_bonus = sum(int(r[3]) for r in recs)
     _say(f"accepted {n_acc} of {B * k}, bonus rows {n_bonus}")
     assert 0 < n_bonus < B  # both the bonus and the rejection paths ran
+
+
+@pytest.mark.parametrize("T", [1.0, 0.8])
+def test_spec_accept_draft_outside_topk(T):
+    """The q == 0 branch (flaxchat/engine.py:548-552): a draft token outside
+    the draft's top-k has draft probability exactly 0, so the target samples
+    from p at once. Rows put such a draft at index 1 (a mid-round
+    rejection, then re-prefill) or at the last index k - 1 (accepted ==
+    k', so a bonus follows: the quirk of engine.py:573); top_k 4 at V =
+    65536. Bit-exact against the oracle."""
+    _say(f"accept q == 0 branch T={T}")
+    B, k, V, seed, top_k = 16, 4, 65536, 77, 4
+    P, Q = _cfg3_logits(B, k, V, seed_np=12)
+    from oracle import sampling as S
+    rnd = np.zeros(B, np.int32)
+    drafts = np.array([[S.draft_sample(Q[b, i], T, top_k, seed, b, 0, i) for i in range(k)] for b in range(B)],
+                      np.int32)
+    # make the target agree with the draft before the planted index, so the
+    # rows reach it: copy the draft logits into the target rows
+    for b in range(B):
+        at = 1 if b % 2 == 0 else k - 1
+        P[b, :at] = Q[b, :at]
+        outside = np.argsort(-Q[b, at], kind="stable")[top_k + 3 + b]
+        drafts[b, at] = outside
+    recs = _check_accept(P, Q, drafts, rnd, T, top_k, seed)
+    hit_mid = sum(1 for b, r in enumerate(recs) if b % 2 == 0 and r[2] == 1 and not r[3])
+    hit_last = sum(1 for b, r in enumerate(recs) if b % 2 == 1 and r[2] == k - 1 and r[3])
+    _say(f"q == 0 at index 1: {hit_mid} of {B // 2} rows; at the last index (+ bonus): {hit_last} of {B // 2}")
+    assert hit_mid == B // 2 and hit_last == B // 2
+
+
+def test_spec_accept_topk_ties_v65536():
+    """top_k 40 at V = 65536 with ties across the cut: logits rounded to a
+    coarse grid so the 40th largest value repeats; the kept set is exactly
+    40 entries, lower index first among equals (lax.top_k,
+    flaxchat/engine.py:461-466). Sampled (T 0.8) and greedy."""
+    from oracle import sampling as S
+    B, k, V, seed, top_k = 32, 4, 65536, 5, 40
+    P, Q = _cfg3_logits(B, k, V, seed_np=13)
+    P = (np.round(P * 2) / 2).astype(np.float32)
+    Q = (np.round(Q * 2) / 2).astype(np.float32)
+    for b in range(B):  # at least one tie straddling the cut in every row
+        v = np.sort(P[b, 0])[::-1][top_k - 1]
+        assert (P[b, 0] == v).sum() > 1
+    rnd = (np.arange(B) % 3).astype(np.int32)
+    for T in (0.8, 0.0):
+        drafts = np.array([[S.draft_sample(Q[b, i], T, top_k, seed, b, int(rnd[b]), i) for i in range(k)]
+                           for b in range(B)], np.int32)
+        recs = _check_accept(P, Q, drafts, rnd, T, top_k, seed)
+        _say(f"top-k ties T={T}: accepted {sum(r[1] for r in recs)} of {B * k}")
 
 
 # ---------------------------------------------------------------- attention prologue
@@ -386,3 +459,63 @@ def test_attn_prologue_vs_oracle(dtype):
         k_exp = _to_kblocked(k_nat) if dtype == "bf16" else k_nat
         np.testing.assert_allclose(k_got, k_exp, rtol=tol, atol=tol)
         np.testing.assert_allclose(v_got, _to_vblocked(v_nat), rtol=tol, atol=tol)
+
+
+# ---------------------------------------------------------------- fused QKV epilogue
+@pytest.mark.parametrize("H,G,M", [(12, 4, 130), (12, 12, 224), (12, 12, 3400)])
+def test_attn_qkv_fused_vs_prologue(H, G, M):
+    """fc_attn_qkv at verify / prefill row counts runs the attention
+    prologue inside the QKV GEMM's epilogue (the 32 x 128 tile of the
+    LDS-shared kernel; at 3400 rows the 256 x 256 tile's quadrants). Its q
+    and the K / V it appends (RoPE, 1.2 * RMSNorm, the value-embedding gate
+    on the V heads) must equal fc_gemm's fp32 projection of the same input
+    followed by fc_attn_prologue, element by element within 1e-2 relative
+    (the outputs are bf16), for a layer with a value embedding and one
+    without. Includes a skipped token (row -1) and one at position cap
+    (q written, nothing appended)."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    from flaxchat_amd.runtime import DeviceCache, DeviceModel
+    from flaxchat_amd.torch_ops import pack_operand
+    _say(f"fused QKV epilogue H={H} G={G} M={M}")
+    D, V, d = 1536, 4096, 128
+    cfg = GPTConfig(sequence_len=1024, vocab_size=V, n_layer=2, n_head=H, n_kv_head=G, n_embd=D,
+                    window_pattern="SL", short_window=256)
+    host = GPT.init_normal_parallel(cfg, seed=9, std=0.05)
+    dm = DeviceModel.from_host(host, dtype="bf16", device=dev())
+    B, cap = 4, 1024
+    rng = np.random.default_rng(M)
+    slots = rng.permutation(B * cap)[:M]
+    rows, pos = (slots // cap).astype(np.int32), (slots % cap).astype(np.int32)
+    rows[3] = -1
+    pos[5] = cap
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev())  # noqa: E731
+    tok_t, row_t, pos_t = i32(rng.integers(0, V, M)), i32(rows), i32(pos)
+    hrows = torch.from_numpy(rng.standard_normal((M, D)).astype(np.float32)).to(dev(), torch.bfloat16)
+    h = pack_operand(hrows)
+    NQKV = (H + 2 * G) * d
+    L = _lib.lib()
+    for layer in range(2):
+        ca, cb = DeviceCache(dm, B, cap), DeviceCache(dm, B, cap)
+        qa = torch.zeros(M, H, d, dtype=torch.bfloat16, device=dev())
+        qb = torch.zeros_like(qa)
+        need = L.fc_attn_qkv_workspace_bytes(ctypes.byref(dm.desc), M, M)
+        assert need == 0, "this row count should take the fused epilogue"
+        check(L.fc_attn_qkv(ctypes.byref(dm.desc), layer, ctypes.byref(ca.desc), h.data_ptr(), tok_t.data_ptr(),
+                            row_t.data_ptr(), pos_t.data_ptr(), M, M, qa.data_ptr(), None, 0, stream()), "attn_qkv")
+        qkv = torch.zeros(M, NQKV, dtype=torch.float32, device=dev())
+        check(L.fc_gemm(h.data_ptr(), dm.t["layers"][layer]["wqkv"].data_ptr(), qkv.data_ptr(), M, NQKV, D,
+                        _lib.FC_BF16, 0, stream()), "gemm")
+        check(L.fc_attn_prologue(ctypes.byref(dm.desc), layer, ctypes.byref(cb.desc), qkv.data_ptr(), h.data_ptr(),
+                                 tok_t.data_ptr(), row_t.data_ptr(), pos_t.data_ptr(), M, qb.data_ptr(), stream()),
+              "prologue")
+        torch.cuda.synchronize()
+        for name, a, b in (("q", qa, qb), ("k", ca.k[layer], cb.k[layer]), ("v", ca.v[layer], cb.v[layer])):
+            a, b = a.float(), b.float()
+            scale = b.abs().max().item()
+            err = (a - b).abs().max().item()
+            rel = ((a - b).abs() / (b.abs() + 1e-2 * scale)).max().item()
+            _say(f"  layer {layer} {name}: max |diff| {err:.3e} (max |ref| {scale:.3f}), max rel {rel:.3e}")
+            assert scale > 0 and rel <= 1e-2, f"layer {layer} {name}"
+        # the skipped token (row -1) wrote no q either
+        assert qa[3].abs().sum().item() == 0 and qb[3].abs().sum().item() == 0
