@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma(const bf16_t* __restrict_
 // once per block; the waves are merged block by block. grid (key split,
 // row x KV group, group of QB query blocks).
 template <int NW, int QB>
-__global__ __launch_bounds__(64 * NW) void k_attn_mfma_qb(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_mfma_qb(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
                                                        const bf16_t* __restrict__ vc, float* __restrict__ part_o,
                                                        float* __restrict__ part_ml, bf16_t* __restrict__ y, int H,
                                                        int G, int cap, const int* __restrict__ row_off,
@@ -400,7 +400,6 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma_qb(const bf16_t* __restri
   bool cvalid[QB];
   int pos_c[QB], lo_c[QB];
   uint4 qf[QB][4];
-  const uint4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int u = 0; u < QB; ++u) {
     const int col = (qb0 + u) * 16 + c;
@@ -409,8 +408,15 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma_qb(const bf16_t* __restri
     pos_c[u] = s0 + j;
     lo_c[u] = window > 0 ? max(0, pos_c[u] - window) : 0;
     const bf16_t* qr = q + ((int64_t)(base + (cvalid[u] ? j : 0)) * H + (cvalid[u] ? head : 0)) * HD + 8 * g4;
+    // load from the (always valid, clamped) address, then mask the value: a
+    // select between the load and `zero` becomes a select of pointers, one of
+    // them to a private copy of `zero`, and the loads turn into flat loads
+    const uint32_t keep = cvalid[u] ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[u][s] = cvalid[u] ? *(const uint4*)(qr + 32 * s) : zero;
+    for (int s = 0; s < 4; ++s) {
+      const uint4 v = *(const uint4*)(qr + 32 * s);
+      qf[u][s] = uint4{v.x & keep, v.y & keep, v.z & keep, v.w & keep};
+    }
   }
   const bf16_t* kbase = kc + (int64_t)bg * cap * HD;
   const bf16_t* vbase = vc + (int64_t)bg * (cap / 32) * HD * 32;
@@ -453,58 +459,61 @@ __global__ __launch_bounds__(64 * NW) void k_attn_mfma_qb(const bf16_t* __restri
   // unnormalised partial and its (max, sum) go to k_attn_combine.
   __shared__ float sm[NW][16], sl[NW][16];
   __shared__ float so[NW][16][HD + 4];
+  // (a guard instead of a break keeps the loop unrolled, so m_run / l_run / O
+  // stay in registers: a runtime index would put them in scratch memory)
 #pragma unroll
   for (int u = 0; u < QB; ++u) {
-    if (u >= nblk) break;  // uniform over the workgroup
-    const int qb = qb0 + u;
-    const int64_t pidx = ((int64_t)bg * nqblk + qb) * nsplit + split;
-    float l_tot = l_run[u] + __shfl_xor(l_run[u], 16, WAVE);
-    l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
-    if (u > 0) __syncthreads();  // the previous block's readers are done with the LDS
-    if (g4 == 0) {
-      sm[wave][c] = m_run[u];
-      sl[wave][c] = l_tot;
-    }
-#pragma unroll
-    for (int db = 0; db < 8; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) so[wave][c][16 * db + 4 * g4 + i] = O[u][db][i];
-    __syncthreads();
-    if (threadIdx.x < 256) {
-      const int qc = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w][qc]);
-      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      float L = 0.f;
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          const float a = exp2f(sm[w][qc] - M);
-          L += a * sl[w][qc];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] += a * so[w][qc][d0 + i];
-        }
+    if (u < nblk) {  // uniform over the workgroup
+      const int qb = qb0 + u;
+      const int64_t pidx = ((int64_t)bg * nqblk + qb) * nsplit + split;
+      float l_tot = l_run[u] + __shfl_xor(l_run[u], 16, WAVE);
+      l_tot = l_tot + __shfl_xor(l_tot, 32, WAVE);
+      if (u > 0) __syncthreads();  // the previous block's readers are done with the LDS
+      if (g4 == 0) {
+        sm[wave][c] = m_run[u];
+        sl[wave][c] = l_tot;
       }
-      const int colq = qb * 16 + qc;
-      if (nsplit == 1) {
-        if (colq < ncol) {
-          const int jq = colq / rep, hq = g * rep + (colq - jq * rep);
-          const float inv = L > 0.f ? 1.f / L : 0.f;
-          uint4 pk;
-          pk.x = pack2bf(o[0] * inv, o[1] * inv);
-          pk.y = pack2bf(o[2] * inv, o[3] * inv);
-          pk.z = pack2bf(o[4] * inv, o[5] * inv);
-          pk.w = pack2bf(o[6] * inv, o[7] * inv);
-          *(uint4*)(y + frag_idx(base + jq, hq * HD + d0, H * HD)) = pk;
+  #pragma unroll
+      for (int db = 0; db < 8; ++db)
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) so[wave][c][16 * db + 4 * g4 + i] = O[u][db][i];
+      __syncthreads();
+      if (threadIdx.x < 256) {
+        const int qc = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+        float M = -INFINITY;
+  #pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w][qc]);
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float L = 0.f;
+        if (M != -INFINITY) {
+  #pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const float a = exp2f(sm[w][qc] - M);
+            L += a * sl[w][qc];
+  #pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] += a * so[w][qc][d0 + i];
+          }
         }
-      } else {
-        float4* po = (float4*)(part_o + (pidx * 16 + qc) * HD + d0);
-        po[0] = make_float4(o[0], o[1], o[2], o[3]);
-        po[1] = make_float4(o[4], o[5], o[6], o[7]);
-        if (d0 == 0) {
-          part_ml[(pidx * 16 + qc) * 2 + 0] = M;
-          part_ml[(pidx * 16 + qc) * 2 + 1] = L;
+        const int colq = qb * 16 + qc;
+        if (nsplit == 1) {
+          if (colq < ncol) {
+            const int jq = colq / rep, hq = g * rep + (colq - jq * rep);
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            uint4 pk;
+            pk.x = pack2bf(o[0] * inv, o[1] * inv);
+            pk.y = pack2bf(o[2] * inv, o[3] * inv);
+            pk.z = pack2bf(o[4] * inv, o[5] * inv);
+            pk.w = pack2bf(o[6] * inv, o[7] * inv);
+            *(uint4*)(y + frag_idx(base + jq, hq * HD + d0, H * HD)) = pk;
+          }
+        } else {
+          float4* po = (float4*)(part_o + (pidx * 16 + qc) * HD + d0);
+          po[0] = make_float4(o[0], o[1], o[2], o[3]);
+          po[1] = make_float4(o[4], o[5], o[6], o[7]);
+          if (d0 == 0) {
+            part_ml[(pidx * 16 + qc) * 2 + 0] = M;
+            part_ml[(pidx * 16 + qc) * 2 + 1] = L;
+          }
         }
       }
     }
@@ -648,7 +657,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(const bf16_t* __restrict__ q
         pk[g4] = uint2{pack2bf(pv[4 * g4], pv[4 * g4 + 1]), pack2bf(pv[4 * g4 + 2], pv[4 * g4 + 3])};    \
       _Pragma("unroll") for (int dd = 0; dd < 4; ++dd) O[dd] *= alpha;                                     \
       _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                   \
-        const uint2 mine = pk[2 * kh + hl], give = pk[2 * kh + 1 - hl];                                    \
+        /* selects, not pk[... + hl]: a lane-dependent index puts pk in scratch */                       \
+        const uint2 mine = hl ? pk[2 * kh + 1] : pk[2 * kh], give = hl ? pk[2 * kh] : pk[2 * kh + 1];      \
         uint2 got;                                                                                         \
         got.x = __shfl_xor(give.x, 32, WAVE);                                                              \
         got.y = __shfl_xor(give.y, 32, WAVE);                                                              \
