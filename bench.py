@@ -143,6 +143,31 @@ def copy_ceiling(dev, n_bytes=1 << 30, n_rep=5):
     return gbs
 
 
+def read_ceiling(dev, n_bytes=1 << 30, n_rep=5):
+    """Measured HBM read ceiling: fc_read_probe (16-byte non-temporal loads,
+    a streaming read with nothing written) over `n_bytes`, the best of a few
+    grid sizes, rated by the bytes it reads."""
+    import torch
+    from flaxchat_amd import _lib
+    src = torch.empty(n_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(4 * 16384, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev)
+    best = 0.0
+    for wgs in (1024, 2048, 4096, 8192, 16384):
+        run = lambda: _lib.check(_lib.lib().fc_read_probe(src.data_ptr(), n_bytes, out.data_ptr(), wgs,  # noqa: E731
+                                                          s.cuda_stream), "fc_read_probe")
+        run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(n_rep):
+            run()
+        e1.record(s)
+        e1.synchronize()
+        best = max(best, n_bytes * n_rep / (e0.elapsed_time(e1) / 1e3) / 1e9)
+    del src, out
+    return best
+
+
 def gemm_calibration(n_iter=20, n_copies=4):
     """fc_gemm (fragment-order operands, store epilogue) against torch.matmul
     (hipBLASLt) on the cfg4 engine's GEMM shapes; `n_copies` weight copies are
@@ -184,7 +209,8 @@ def gemm_calibration(n_iter=20, n_copies=4):
     return out
 
 
-def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0):
+def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0, at_position=None, p_reject=None,
+                 accepted=None):
     """The oracle's literal-mode generate_speculative on host cores."""
     from flaxchat_amd.runtime import to_host
     from oracle.spec import spec_literal
@@ -202,11 +228,36 @@ def cpu_baseline(dm_t, dm_d, cfg_name, seed, k, temperature, budget_s=25.0):
     out = spec_literal(ht, hd, prompt, max_tokens=new, temperature=temperature, top_k=None, seed=seed,
                        draft_steps=k)
     dt = time.perf_counter() - t0
-    return {"value": round((len(out) - len(prompt)) / dt, 4), "unit": "tokens/s", "cores": int(cores),
-            "kind": "port",
-            "sample": f"oracle spec_literal (restatement of flaxchat/engine.py:410-608, fp32 numpy) on the "
-                      f"{cfg_name} architecture and weights, batch 1, prompt 64 ids (not the full prompt), "
-                      f"{new} new tokens, k={k}, T={temperature}, including prefill; {dt:.1f} s"}
+    res = {"value": round((len(out) - len(prompt)) / dt, 4), "unit": "tokens/s", "cores": int(cores),
+           "kind": "port",
+           "sample": f"oracle spec_literal (restatement of flaxchat/engine.py:410-608, fp32 numpy) on the "
+                     f"{cfg_name} architecture and weights, batch 1, prompt 64 ids (not the full prompt), "
+                     f"{new} new tokens, k={k}, T={temperature}, including prefill; {dt:.1f} s"}
+    if at_position and p_reject is not None and accepted is not None:
+        # one per-token forward of each model at the workload's context length
+        # (the cache holds zeros: the cost does not depend on the values)
+        from oracle.model import OracleModel
+        cost = {}
+        for name, m in (("target", ht), ("draft", hd)):
+            om = OracleModel(m)
+            st = om.new_state(at_position + 8)
+            om.step(1, at_position - 1, st)
+            t1 = time.perf_counter()
+            for i in range(3):
+                om.step(2 + i, at_position + i, st)
+            cost[name] = (time.perf_counter() - t1) / 3
+        # the literal loop per round: k draft steps, k target steps, and on a
+        # mid-round rejection a re-prefill of both models over the whole
+        # sequence (flaxchat/engine.py:492-523, 593-606)
+        round_s = k * (cost["draft"] + cost["target"]) + p_reject * at_position * (cost["draft"] + cost["target"])
+        res["per_token_forward_ms_at_context"] = {"context": at_position, "target": round(cost["target"] * 1e3, 1),
+                                                  "draft": round(cost["draft"] * 1e3, 1)}
+        res["estimate_at_context"] = {
+            "tokens_per_s": round(accepted / round_s, 5),
+            "how": f"extrapolated, not measured: per round {k} draft + {k} target forwards plus, with the "
+                   f"GPU run's mid-round rejection rate {p_reject:.2f}, a re-prefill of both models over "
+                   f"{at_position} positions; {accepted:.2f} tokens per round (the GPU run's mean)"}
+    return res
 
 
 def main():
@@ -279,23 +330,40 @@ def main():
     acc = np.concatenate(sess.accept_hist) if sess.accept_hist else np.zeros(1)
     print(f"[bench] {steps} rounds {toks} tokens {el:.3f}s mean accepted/round {acc.mean():.2f}",
           file=sys.stderr, flush=True)
+    # the rest of the run (to every row's max_tokens) and the whole timed + rest
+    # figure: tail rounds still pay for finished rows
+    t1 = time.perf_counter()
+    sess.run()
+    sess.stream.synchronize()
+    el_all = el + (time.perf_counter() - t1)
+    steps_all = sess.rounds - rounds_before
+    toks_all = sess.emitted_tokens() - done_before
+    full_run = {"rounds": int(steps_all), "tokens": int(toks_all), "ms_per_round": round(el_all / max(steps_all, 1) * 1e3, 3),
+                "tokens_per_s": round(toks_all / el_all, 2),
+                "what": "timed window plus the remaining rounds until every row has max_tokens"}
+    acc_all = np.concatenate(sess.accept_hist) if sess.accept_hist else np.zeros(1)
+    p_reject = float(np.mean(acc_all < k)) if sess.accept_hist else None
+    print(f"[bench] full run: {steps_all} rounds {toks_all} tokens {el_all:.3f}s", file=sys.stderr, flush=True)
 
     roof = None
     if not args.no_roofline:
         r = attention_roofline(sess)
         ceil = copy_ceiling(target.device)
+        rceil = read_ceiling(target.device)
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
                 "kernel": "k_attn_mfma (verify, k+1 queries per row, one key split)",
                 "per_launch_bytes": int(r["per_launch_bytes"]), "per_launch_us": round(r["per_launch_us"], 2),
                 "S_layer": r["S"], "L_layer": r["L"],
-                "copy_ceiling": round(ceil, 1), "frac_of_copy_ceiling": round(r["achieved"] / ceil, 4)}
-        print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s)", file=sys.stderr,
-              flush=True)
+                "copy_ceiling": round(ceil, 1), "frac_of_copy_ceiling": round(r["achieved"] / ceil, 4),
+                "read_ceiling": round(rceil, 1), "frac_of_read_ceiling": round(r["achieved"] / rceil, 4)}
+        print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
+              f"1 GiB streaming read: {rceil:.0f} GB/s)", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(target, draft, args.config, seed, k, temp)
+        cpu = cpu_baseline(target, draft, args.config, seed, k, temp, at_position=P, p_reject=p_reject,
+                           accepted=float(acc_all.mean()))
     out = {
         "metric": "spec-decode accepted tokens/s (d24+d4, bs32); verify-attn % HBM peak",
         "value": round(toks / el, 2), "unit": "tokens/s", "n_gpus": 1, "steps": int(steps),
@@ -308,6 +376,7 @@ def main():
                    "global_batch": B, "seq_len": P + new, "parallelism": "single GPU",
                    "graph": not args.no_graph},
         "mean_accepted_per_round": round(float(acc.mean()), 3),
+        "full_run": full_run,
         "prefill_s": round(prefill_s, 3),
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -527,3 +527,36 @@ extern "C" int32_t fc_attn_qkv(const fc_model* m, int32_t layer, const fc_cache*
   if (rc) return rc;
   return fc_launch_prologue((const float*)work, h, tokens, m, layer, c, tok_row, tok_pos, M, nullptr, q, s);
 }
+
+// Streaming read of `bytes` bytes (the measured read ceiling the benchmark
+// rates the HBM-bound kernels against): 16-byte non-temporal loads, four in
+// flight per thread, folded with xor into one word per wave so the loads
+// cannot be dropped.
+typedef uint32_t rp_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_read_probe(const rp_u32x4* __restrict__ src, int64_t n16,
+                                                    uint32_t* __restrict__ out) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  rp_u32x4 acc = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const rp_u32x4 a = __builtin_nontemporal_load(src + i), b = __builtin_nontemporal_load(src + i + stride);
+    const rp_u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const rp_u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+  uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o, WAVE);
+  if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = x;
+}
+
+extern "C" int32_t fc_read_probe(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups, void* stream) {
+  FC_CHECK_ARG(src && out, "null pointer");
+  FC_CHECK_ARG(bytes > 0 && bytes % 16 == 0, "bytes must be a positive multiple of 16");
+  FC_CHECK_ARG(workgroups > 0 && workgroups <= 65536, "workgroups in [1, 65536]");
+  hipLaunchKernelGGL(k_read_probe, dim3(workgroups), dim3(256), 0, (hipStream_t)stream, (const rp_u32x4*)src,
+                     bytes / 16, out);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}
