@@ -270,6 +270,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-full-run", action="store_true",
+                    help="stop after the timed rounds (profiling passes); full_run is then null")
     ap.add_argument("--gemm-calibration", action="store_true",
                     help="time fc_gemm against torch.matmul (hipBLASLt) on the cfg4 GEMM shapes and exit")
     ap.add_argument("--roofline-only", action="store_true",
@@ -332,18 +334,21 @@ def main():
           file=sys.stderr, flush=True)
     # the rest of the run (to every row's max_tokens) and the whole timed + rest
     # figure: tail rounds still pay for finished rows
-    t1 = time.perf_counter()
-    sess.run()
-    sess.stream.synchronize()
-    el_all = el + (time.perf_counter() - t1)
-    steps_all = sess.rounds - rounds_before
-    toks_all = sess.emitted_tokens() - done_before
-    full_run = {"rounds": int(steps_all), "tokens": int(toks_all), "ms_per_round": round(el_all / max(steps_all, 1) * 1e3, 3),
-                "tokens_per_s": round(toks_all / el_all, 2),
-                "what": "timed window plus the remaining rounds until every row has max_tokens"}
+    full_run = None
+    if not args.no_full_run:
+        t1 = time.perf_counter()
+        sess.run()
+        sess.stream.synchronize()
+        el_all = el + (time.perf_counter() - t1)
+        steps_all = sess.rounds - rounds_before
+        toks_all = sess.emitted_tokens() - done_before
+        full_run = {"rounds": int(steps_all), "tokens": int(toks_all),
+                    "ms_per_round": round(el_all / max(steps_all, 1) * 1e3, 3),
+                    "tokens_per_s": round(toks_all / el_all, 2),
+                    "what": "timed window plus the remaining rounds until every row has max_tokens"}
+        print(f"[bench] full run: {steps_all} rounds {toks_all} tokens {el_all:.3f}s", file=sys.stderr, flush=True)
     acc_all = np.concatenate(sess.accept_hist) if sess.accept_hist else np.zeros(1)
     p_reject = float(np.mean(acc_all < k)) if sess.accept_hist else None
-    print(f"[bench] full run: {steps_all} rounds {toks_all} tokens {el_all:.3f}s", file=sys.stderr, flush=True)
 
     roof = None
     if not args.no_roofline:
