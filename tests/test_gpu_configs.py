@@ -100,7 +100,7 @@ def _session(target, draft, name):
 
 def _check_first_round(s, name):
     """Round 1's device inputs to the accept step, replayed on the host."""
-    from oracle.sampling import accept_round, get_probs
+    from oracle.sampling import accept_round, draft_sample, get_probs
     _, _, B, P, new, k, T, top_k, seed = FULL[name]
     rnd0 = s.bufs["round"].cpu().numpy().copy()
     assert (rnd0 == 0).all()
@@ -113,6 +113,12 @@ def _check_first_round(s, name):
     for b in range(B):
         p = s.bufs["p_logits"][b].cpu().numpy()
         q = s.bufs["q_logits"][b].cpu().numpy()
+        # the drafts are the oracle's draws from the device's draft logits
+        # (flaxchat/engine.py:492-499: the multi-workgroup vocab pass of each
+        # draft step and its per-row merge)
+        if b < 8:
+            ref_d = [draft_sample(q[i], T, top_k, seed, b, 0, i) for i in range(k)]
+            assert drafts[b].tolist() == ref_d, f"row {b}: drafts {drafts[b].tolist()} vs oracle {ref_d}"
         em, acc, rej, bonus = accept_round(p, q, drafts[b], T, top_k, seed, b, 0)
         n = int(res[b, 0])
         assert res[b, 8:8 + n].tolist() == em, f"row {b}: device {res[b, 8:8 + n].tolist()} vs oracle {em}"
