@@ -384,6 +384,311 @@ __global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i) {
   if (threadIdx.x == 0) place_draft(s, b, i, tok);
 }
 
+// ---------------------------------------------------------------------------
+// Top-k rows split over many workgroups (0 < top_k <= TK_MAX, T > 0): every
+// 1024-entry chunk of a row keeps its own top-k candidates (larger value
+// first, lower index first among equal values), the row's keep set being a
+// subset of their union (an entry with top_k entries ahead of it in its own
+// chunk has them ahead of it in the row); then one workgroup per row selects
+// the keep set among the candidates and computes the statistics. For a draw (Gumbel-max over
+// log(max(p, 1e-10)) + G, flaxchat/engine.py:478-482) the candidates are
+// scored with their own noise; every other entry has p = 0, so a chunk only
+// reports the largest G among its non-candidates.
+// ---------------------------------------------------------------------------
+#define TK_EPL 16                 // entries per lane of the chunk pass
+#define TK_CH (64 * TK_EPL)       // entries per chunk (one wave)
+#define TK_MAX 64                 // candidates per chunk: top_k <= TK_MAX
+#define TK_NCH 64                 // chunks per row: V <= TK_NCH * TK_CH
+#define TK_THR 256
+#define TK_SPT (TK_NCH * TK_MAX / TK_THR)  // candidate slots per thread of the per-row pass
+struct TkChunk {      // one chunk of one row
+  float g; int gi;    // largest G among the chunk's non-candidates (draw only) and its index
+  int n, pad;         // candidates kept (min(top_k, entries in the chunk))
+  float z[TK_MAX];    // candidates in index order, their indices and (draw) their G
+  int idx[TK_MAX];
+  float gz[TK_MAX];
+};
+
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+// exclusive prefix sum over the wave's lanes
+__device__ __forceinline__ int wave_excl(int v) {
+  const int lane = threadIdx.x & 63;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, WAVE);
+    if (lane >= o) x += y;
+  }
+  return x - v;
+}
+
+// The kk-th largest order-preserving key among a wave's entries (N per lane,
+// `ok` marks real ones): the largest t with #{key >= t} >= kk, by a 32-step
+// binary search counted with wave sums; also #{key > t}. Uniform over the wave.
+template <int N>
+__device__ __forceinline__ uint32_t wave_kth_key(const float (&v)[N], const bool (&ok)[N], int kk, int& ngt) {
+  uint32_t lo = 0u, hi = 0xffffffffu;
+  while (lo < hi) {
+    const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < N; ++q) n += ok[q] && mono(v[q]) >= mid;
+    if (wave_isum(n) >= kk) lo = mid;
+    else hi = mid - 1u;
+  }
+  int g = 0;
+#pragma unroll
+  for (int q = 0; q < N; ++q) g += ok[q] && mono(v[q]) > lo;
+  ngt = wave_isum(g);
+  return lo;
+}
+
+// Keep flags of a wave's entries (index order = (lane, q) order) for the
+// threshold key tau: every entry above it and the first need equal to it;
+// *last_eq = the index of the need-th equal entry (written by its lane).
+template <int N>
+__device__ __forceinline__ void wave_keep(const float (&v)[N], const bool (&ok)[N], const int (&idx)[N], uint32_t tau,
+                                          int need, bool (&in)[N], int* last_eq) {
+  int neq = 0;
+#pragma unroll
+  for (int q = 0; q < N; ++q) neq += ok[q] && mono(v[q]) == tau;
+  int eq_before = wave_excl(neq);
+#pragma unroll
+  for (int q = 0; q < N; ++q) {
+    in[q] = false;
+    if (ok[q]) {
+      const uint32_t k = mono(v[q]);
+      if (k > tau) {
+        in[q] = true;
+      } else if (k == tau) {
+        ++eq_before;
+        in[q] = eq_before <= need;
+        if (last_eq != nullptr && eq_before == need) *last_eq = idx[q];
+      }
+    }
+  }
+}
+
+// Candidates of chunks 4 blockIdx.x + wave of logits row blockIdx.y, one
+// wave per chunk (lane l holds entries TK_EPL l .. + TK_EPL - 1). With
+// `draw`, the G of every entry (counter (entry / 4, row, round[row], slot)):
+// kept with the candidates, and the largest among the rest.
+__global__ __launch_bounds__(TK_THR) void k_topk_cand(const float* __restrict__ z0, int64_t row_stride, int V,
+                                                      int top_k, int draw, uint64_t seed, const int* __restrict__ round,
+                                                      int slot, int nch, TkChunk* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * (TK_THR / 64) + wave, r = blockIdx.y;
+  if (c >= nch) return;  // the whole wave
+  const float* z = z0 + (int64_t)r * row_stride;
+  const int e0 = c * TK_CH + lane * TK_EPL;
+  float v[TK_EPL];
+  bool ok[TK_EPL];
+  int idx[TK_EPL];
+  const bool vec = ((uintptr_t)z % 16 == 0) && e0 + TK_EPL - 1 < V;
+#pragma unroll
+  for (int q = 0; q < TK_EPL; q += 4) {
+    if (vec) {
+      const float4 t = *(const float4*)(z + e0 + q);
+      v[q] = t.x; v[q + 1] = t.y; v[q + 2] = t.z; v[q + 3] = t.w;
+    } else {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[q + w] = e0 + q + w < V ? z[e0 + q + w] : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < TK_EPL; ++q) {
+    ok[q] = e0 + q < V;
+    idx[q] = e0 + q;
+  }
+  const int kk = min(top_k, V - c * TK_CH);
+  int ngt;
+  const uint32_t tau = wave_kth_key<TK_EPL>(v, ok, kk, ngt);
+  bool in[TK_EPL];
+  wave_keep<TK_EPL>(v, ok, idx, tau, kk - ngt, in, nullptr);
+  int nin = 0;
+#pragma unroll
+  for (int q = 0; q < TK_EPL; ++q) nin += in[q];
+  int pos = wave_excl(nin);
+  TkChunk* o = out + (int64_t)r * nch + c;
+  float bg = -INFINITY;
+  int bgi = 0x7fffffff;
+  const int rnd = draw ? round[r] : 0;
+#pragma unroll
+  for (int q = 0; q < TK_EPL; q += 4) {
+    u32x4 rr = {0u, 0u, 0u, 0u};
+    if (draw)
+      rr = philox4x32_10(u32x4{(uint32_t)((e0 + q) >> 2), (uint32_t)r, (uint32_t)rnd, (uint32_t)slot},
+                         (uint32_t)seed, (uint32_t)(seed >> 32));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float G = draw ? gumbel_of(pick(rr, w)) : 0.f;
+      if (in[q + w]) {
+        o->z[pos] = v[q + w];
+        o->idx[pos] = e0 + q + w;
+        o->gz[pos] = G;
+        ++pos;
+      } else if (draw && ok[q + w]) {
+        argmax_merge(bg, bgi, G, e0 + q + w);
+      }
+    }
+  }
+  wave_argmax(bg, bgi);
+  if (lane == 0) {
+    o->g = bg;
+    o->gi = bgi;
+    o->n = kk;
+  }
+}
+
+// Keep set and statistics of one logits row from its chunks' candidates, by
+// one workgroup (row_stats_block's result; tie_idx is the last kept index
+// equal to tau): the binary search over the candidate keys counted over the
+// block; with `draw`, the Gumbel-max token from the candidates' stored G and
+// the chunks' largest G outside them (p = 0 there: log(1e-10) + G).
+struct TkRow {
+  fc_rowstat st;
+  int tok;
+};
+__device__ __forceinline__ TkRow tk_finish_row(const TkChunk* __restrict__ ch, int nch, int V, int top_k, float T,
+                                               bool draw) {
+  __shared__ int red[2][TK_THR / 64];
+  __shared__ int tie_sm;
+  __shared__ float redv[16];
+  __shared__ int redi[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // slot q of thread t: candidate j of chunk cc for t TK_SPT + q = cc TK_MAX + j (index order)
+  float zv[TK_SPT], gv[TK_SPT];
+  int iv[TK_SPT];
+  bool ok[TK_SPT];
+#pragma unroll
+  for (int q = 0; q < TK_SPT; ++q) {
+    const int sidx = threadIdx.x * TK_SPT + q, cc = sidx / TK_MAX, j = sidx - cc * TK_MAX;
+    ok[q] = cc < nch && j < ch[cc].n;
+    zv[q] = ok[q] ? ch[cc].z[j] : -INFINITY;
+    iv[q] = ok[q] ? ch[cc].idx[j] : 0x7fffffff;
+    gv[q] = ok[q] && draw ? ch[cc].gz[j] : 0.f;
+  }
+  const int kk = min(top_k, V);
+  uint32_t lo = 0u, hi = 0xffffffffu;
+  int it = 0;
+  while (lo < hi) {  // the same sequence in every thread
+    const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < TK_SPT; ++q) n += ok[q] && mono(zv[q]) >= mid;
+    n = wave_isum(n);
+    if (lane == 0) red[it & 1][wave] = n;  // alternating buffers: one barrier per step
+    __syncthreads();
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < TK_THR / 64; ++w) tot += red[it & 1][w];
+    if (tot >= kk) lo = mid;
+    else hi = mid - 1u;
+    ++it;
+  }
+  const uint32_t tau = lo;
+  int ngt = 0, neq = 0;
+#pragma unroll
+  for (int q = 0; q < TK_SPT; ++q) {
+    ngt += ok[q] && mono(zv[q]) > tau;
+    neq += ok[q] && mono(zv[q]) == tau;
+  }
+  const int wgt = wave_isum(ngt), weq_ex = wave_excl(neq), weq = wave_isum(neq);
+  __syncthreads();
+  if (lane == 0) {
+    red[0][wave] = wgt;
+    red[1][wave] = weq;
+  }
+  __syncthreads();
+  int gt = 0, eq_before = weq_ex;
+#pragma unroll
+  for (int w = 0; w < TK_THR / 64; ++w) {
+    gt += red[0][w];
+    if (w < wave) eq_before += red[1][w];
+  }
+  const int need = kk - gt;
+  bool in[TK_SPT];
+#pragma unroll
+  for (int q = 0; q < TK_SPT; ++q) {
+    in[q] = false;
+    if (ok[q]) {
+      const uint32_t k = mono(zv[q]);
+      if (k > tau) {
+        in[q] = true;
+      } else if (k == tau) {
+        ++eq_before;
+        in[q] = eq_before <= need;
+        if (eq_before == need) tie_sm = iv[q];  // exactly one slot of the block
+      }
+    }
+  }
+  __syncthreads();
+  const int tie_idx = tie_sm;
+  float bz = -INFINITY;
+  int bzi = 0x7fffffff;
+#pragma unroll
+  for (int q = 0; q < TK_SPT; ++q)
+    if (in[q]) argmax_merge(bz, bzi, zv[q], iv[q]);
+  block_argmax(bz, bzi, redv, redi);
+  const float mx = bz / T;  // max of z / T over the keep set
+  float sum = 0.f;
+#pragma unroll
+  for (int q = 0; q < TK_SPT; ++q)
+    if (in[q]) sum += expf(zv[q] / T - mx);
+  sum = block_sum(sum, redv);
+  TkRow res;
+  res.st = fc_rowstat{};
+  res.st.mx = mx;
+  res.st.sum = sum;
+  res.st.tau = unmono(tau);
+  res.st.tie_idx = tie_idx;
+  res.st.argmax = bzi;
+  res.tok = bzi;
+  if (draw) {
+    const float lfl = logf(1e-10f);
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < TK_SPT; ++q)
+      if (ok[q]) {
+        const float p = in[q] ? expf(zv[q] / T - mx) / sum : 0.f;
+        argmax_merge(bv, bi, logf(fmaxf(p, 1e-10f)) + gv[q], iv[q]);
+      }
+    for (int cc = threadIdx.x; cc < nch; cc += TK_THR) argmax_merge(bv, bi, lfl + ch[cc].g, ch[cc].gi);
+    block_argmax(bv, bi, redv, redi);
+    res.tok = bi;
+  }
+  return res;
+}
+
+// Draft step i with a top-k filter: statistics and proposal d_{i+1}, one
+// workgroup per row.
+__global__ __launch_bounds__(TK_THR) void k_topk_draft(SpecDev s, int i, const TkChunk* __restrict__ ch, int nch) {
+  const int b = blockIdx.x;
+  const TkRow r = tk_finish_row(ch + (int64_t)b * nch, nch, s.V, s.top_k, s.T, true);
+  if (threadIdx.x == 0) {
+    s.q_stats[b * s.k + i] = r.st;
+    place_draft(s, b, i, r.tok);
+  }
+}
+
+// Statistics of each logits row (the target's k+1 rows per row), one workgroup per row.
+__global__ __launch_bounds__(TK_THR) void k_topk_stats(const TkChunk* __restrict__ ch, int nch, int rows, int V,
+                                                       int top_k, float T, fc_rowstat* __restrict__ stats) {
+  const int r = blockIdx.x;
+  const TkRow t = tk_finish_row(ch + (int64_t)r * nch, nch, V, top_k, T, false);
+  if (threadIdx.x == 0) stats[r] = t.st;
+}
+
+static bool tk_fast(const fc_spec_state* st) {
+  return st->top_k > 0 && st->top_k <= TK_MAX && (st->vocab + TK_CH - 1) / TK_CH <= TK_NCH;
+}
+static int tk_nch(int V) { return (V + TK_CH - 1) / TK_CH; }
+
 // The rollback state machine after one accept/reject pass: append the
 // emitted tokens, move the cache lengths and pending tokens of both models,
 // and fill the row's result record.
@@ -978,6 +1283,7 @@ struct PartLayout {
   Decision* ctl;
   VPart* vp;
   DPart* dp;
+  TkChunk* tk;  // top-k candidates of up to batch x (k + 1) rows
   int64_t bytes;
 };
 static PartLayout part_layout(void* base, int B, int K, int V) {
@@ -985,11 +1291,13 @@ static PartLayout part_layout(void* base, int B, int K, int V) {
   PartLayout L;
   const int64_t o_vp = fc_align((int64_t)B * sizeof(Decision));
   const int64_t o_dp = o_vp + fc_align((int64_t)B * (K + 1) * nch1 * sizeof(VPart));
-  L.bytes = o_dp + fc_align((int64_t)B * 2 * nch1 * sizeof(DPart));
+  const int64_t o_tk = o_dp + fc_align((int64_t)B * 2 * nch1 * sizeof(DPart));
+  L.bytes = o_tk + fc_align((int64_t)B * (K + 1) * tk_nch(V) * sizeof(TkChunk));
   char* p = (char*)base;
   L.ctl = (Decision*)p;
   L.vp = (VPart*)(p + o_vp);
   L.dp = (DPart*)(p + o_dp);
+  L.tk = (TkChunk*)(p + o_tk);
   return L;
 }
 
@@ -1025,8 +1333,19 @@ extern "C" int32_t fc_spec_accept(const fc_spec_state* st, void* stream) {
   SpecDev d = to_dev(st);
   const int B = st->batch, K = st->k, V = st->vocab;
   if (!chunked(st)) {
-    rc = fc_launch_row_stats(st->p_logits, B * (K + 1), V, st->temperature, st->top_k, st->p_stats, s);
-    if (rc) return rc;
+    if (tk_fast(st)) {  // the target rows' keep sets from per-chunk candidates
+      const PartLayout L = part_layout(st->part, B, K, V);
+      const int nc = tk_nch(V);
+      hipLaunchKernelGGL(k_topk_cand, dim3((nc + 3) / 4, B * (K + 1)), dim3(TK_THR), 0, s, st->p_logits, (int64_t)V,
+                         V, st->top_k, 0, st->seed, st->round, 0, nc, L.tk);
+      FC_LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_topk_stats, dim3(B * (K + 1)), dim3(TK_THR), 0, s, L.tk, nc, B * (K + 1), V,
+                         st->top_k, st->temperature, st->p_stats);
+      FC_LAUNCH_CHECK();
+    } else {
+      rc = fc_launch_row_stats(st->p_logits, B * (K + 1), V, st->temperature, st->top_k, st->p_stats, s);
+      if (rc) return rc;
+    }
     hipLaunchKernelGGL(k_accept, dim3(B), dim3(NTHR), 0, s, d);
     FC_LAUNCH_CHECK();
     return FC_OK;
@@ -1129,6 +1448,12 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
                         st->seed, st->round, i, L.vp, &nch, s);
       if (rc) return rc;
       hipLaunchKernelGGL(k_draft_finish, dim3((B + 3) / 4), dim3(VP_THR), 0, s, d, i, L.vp, nch);
+    } else if (tk_fast(st)) {  // top-k: per-chunk candidates, then one workgroup per row
+      const int nc = tk_nch(V);
+      hipLaunchKernelGGL(k_topk_cand, dim3((nc + 3) / 4, B), dim3(TK_THR), 0, s, st->q_logits + (int64_t)i * V,
+                         (int64_t)K * V, V, st->top_k, 1, st->seed, st->round, i, nc, L.tk);
+      FC_LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_topk_draft, dim3(B), dim3(TK_THR), 0, s, d, i, L.tk, nc);
     } else {
       hipLaunchKernelGGL(k_draft_sample, dim3(B), dim3(NTHR), 0, s, d, i);
     }
