@@ -272,6 +272,8 @@ def main():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-full-run", action="store_true",
                     help="stop after the timed rounds (profiling passes); full_run is then null")
+    ap.add_argument("--no-topk-line", action="store_true",
+                    help="skip the second measurement with the drop-in default top_k=40")
     ap.add_argument("--gemm-calibration", action="store_true",
                     help="time fc_gemm against torch.matmul (hipBLASLt) on the cfg4 GEMM shapes and exit")
     ap.add_argument("--roofline-only", action="store_true",
@@ -365,6 +367,28 @@ def main():
                 "read_ceiling": round(rceil, 1), "frac_of_read_ceiling": round(r["achieved"] / rceil, 4)}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
               f"1 GiB streaming read: {rceil:.0f} GB/s)", file=sys.stderr, flush=True)
+    topk_line = None
+    if not args.no_topk_line and not args.top_k and temp > 0:
+        # the same workload with generate_speculative's default top_k=40
+        # (flaxchat/engine.py:411): same prompts, steps and warm-up
+        s2 = SpecSession(target, draft, prompts, new, temp, 40, seed, k, use_graph=not args.no_graph)
+        s2.prefill()
+        if args.warmup:
+            s2.run(max_rounds=args.warmup)
+        b2, r2 = s2.emitted_tokens(), s2.rounds
+        s2.stream.synchronize()
+        t2 = time.perf_counter()
+        s2.run(max_rounds=args.steps or None)
+        s2.stream.synchronize()
+        e2 = time.perf_counter() - t2
+        n2, k2 = s2.rounds - r2, s2.emitted_tokens() - b2
+        a2 = np.concatenate(s2.accept_hist) if s2.accept_hist else np.zeros(1)
+        topk_line = {"top_k": 40, "rounds": int(n2), "ms_per_round": round(e2 / max(n2, 1) * 1e3, 3),
+                     "tokens_per_s": round(k2 / e2, 2), "mean_accepted_per_round": round(float(a2.mean()), 3)}
+        s2.close()
+        del s2
+        torch.cuda.empty_cache()
+        print(f"[bench] top_k=40: {n2} rounds {k2} tokens {e2:.3f}s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(target, draft, args.config, seed, k, temp, at_position=P, p_reject=p_reject,
@@ -382,6 +406,7 @@ def main():
                    "graph": not args.no_graph},
         "mean_accepted_per_round": round(float(acc.mean()), 3),
         "full_run": full_run,
+        "top_k_default": topk_line,
         "prefill_s": round(prefill_s, 3),
         "roofline": roof,
         "cpu_baseline": cpu,
