@@ -144,9 +144,9 @@ def copy_ceiling(dev, n_bytes=1 << 30, n_rep=5):
 
 
 def read_ceiling(dev, n_bytes=1 << 30, n_rep=5):
-    """Measured HBM read ceiling: fc_read_probe (16-byte non-temporal loads,
-    a streaming read with nothing written) over `n_bytes`, the best of a few
-    grid sizes, rated by the bytes it reads."""
+    """Measured HBM read ceiling: fc_read_probe (each workgroup streams a
+    contiguous share with 16-byte non-temporal loads, nothing written) over
+    `n_bytes`, the best of a few grid sizes, rated by the bytes it reads."""
     import torch
     from flaxchat_amd import _lib
     src = torch.empty(n_bytes, dtype=torch.uint8, device=dev)

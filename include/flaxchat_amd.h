@@ -313,8 +313,9 @@ int32_t fc_cross_entropy(const float* logits, int64_t row_stride, const int32_t*
                          int32_t V, float* loss, void* stream);
 
 /* Streaming read of `bytes` (a multiple of 16) from device memory by
- * `workgroups` workgroups of 256 threads with 16-byte non-temporal loads; out
- * receives 4 * workgroups xor-folded words. No counterpart in the reference:
+ * `workgroups` workgroups of 256 threads, each streaming one contiguous
+ * share with 16-byte non-temporal loads; out receives 4 * workgroups
+ * xor-folded words. No counterpart in the reference:
  * the benchmark's measured read ceiling, against which the HBM-bound kernels
  * are rated next to the 8 TB/s peak. */
 int32_t fc_read_probe(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups, void* stream);
