@@ -403,65 +403,87 @@ __global__ __launch_bounds__(NTHR) void k_draft_sample(SpecDev s, int i) {
 #define TK_SPT (TK_NCH * TK_MAX / TK_THR)  // candidate slots per thread of the per-row pass
 struct TkChunk {      // one chunk of one row
   float g; int gi;    // largest G among the chunk's non-candidates (draw only) and its index
-  int n, pad;         // candidates kept (min(top_k, entries in the chunk))
+  int n;              // candidates kept (min(top_k, entries in the chunk))
+  uint32_t kmax;      // order-preserving key of the chunk's largest entry
   float z[TK_MAX];    // candidates in index order, their indices and (draw) their G
   int idx[TK_MAX];
   float gz[TK_MAX];
 };
 
-__device__ __forceinline__ int wave_isum(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
+// Counts over the wave from ballots (a compare mask and a population
+// count, no cross-lane data movement); every lane of the wave takes part.
+// lanes whose `pred` holds (uniform over the wave)
+__device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
+// lanes below this one whose `pred` holds
+__device__ __forceinline__ int lanes_below(bool pred) {
+  const uint64_t m = __ballot(pred);
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
-// exclusive prefix sum over the wave's lanes
-__device__ __forceinline__ int wave_excl(int v) {
-  const int lane = threadIdx.x & 63;
-  int x = v;
+// exclusive prefix sum over the wave's lanes of v in [0, 2^BITS)
+template <int BITS>
+__device__ __forceinline__ int wave_excl_small(int v) {
+  int r = 0;
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, WAVE);
-    if (lane >= o) x += y;
-  }
-  return x - v;
+  for (int b = 0; b < BITS; ++b) r += lanes_below((v >> b) & 1) << b;
+  return r;
+}
+// sum over the wave's lanes of v in [0, 2^BITS) (uniform)
+template <int BITS>
+__device__ __forceinline__ int wave_sum_small(int v) {
+  int r = 0;
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) r += wave_count((v >> b) & 1) << b;
+  return r;
 }
 
 // The kk-th largest order-preserving key among a wave's entries (N per lane,
-// `ok` marks real ones): the largest t with #{key >= t} >= kk, by a 32-step
-// binary search counted with wave sums; also #{key > t}. Uniform over the wave.
+// `ok` marks real ones), known to lie in [lo, hi]: the largest t with
+// #{key >= t} >= kk, by binary search counted with ballots; also #{key > t}.
+// lo and hi are uniform over the wave, and so is the result.
 template <int N>
-__device__ __forceinline__ uint32_t wave_kth_key(const float (&v)[N], const bool (&ok)[N], int kk, int& ngt) {
-  uint32_t lo = 0u, hi = 0xffffffffu;
+__device__ __forceinline__ uint32_t wave_kth_key(const uint32_t (&key)[N], const bool (&ok)[N], int kk, uint32_t lo,
+                                                 uint32_t hi, int& ngt) {
   while (lo < hi) {
     const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
     int n = 0;
 #pragma unroll
-    for (int q = 0; q < N; ++q) n += ok[q] && mono(v[q]) >= mid;
-    if (wave_isum(n) >= kk) lo = mid;
+    for (int q = 0; q < N; ++q) n += wave_count(ok[q] && key[q] >= mid);
+    if (n >= kk) lo = mid;
     else hi = mid - 1u;
   }
   int g = 0;
 #pragma unroll
-  for (int q = 0; q < N; ++q) g += ok[q] && mono(v[q]) > lo;
-  ngt = wave_isum(g);
+  for (int q = 0; q < N; ++q) g += wave_count(ok[q] && key[q] > lo);
+  ngt = g;
   return lo;
 }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, WAVE));
+  return v;
+}
+// Entries the search keeps after the lower bound: at most this many go
+// through the narrow search (2 per lane of the chunk pass, 4 per lane of the
+// row pass), more take the search over every entry.
+#define TK_NARROW_WAVE 128
+#define TK_NARROW_ROW 256
 
 // Keep flags of a wave's entries (index order = (lane, q) order) for the
 // threshold key tau: every entry above it and the first need equal to it;
 // *last_eq = the index of the need-th equal entry (written by its lane).
 template <int N>
-__device__ __forceinline__ void wave_keep(const float (&v)[N], const bool (&ok)[N], const int (&idx)[N], uint32_t tau,
-                                          int need, bool (&in)[N], int* last_eq) {
+__device__ __forceinline__ void wave_keep(const uint32_t (&key)[N], const bool (&ok)[N], const int (&idx)[N],
+                                          uint32_t tau, int need, bool (&in)[N], int* last_eq) {
   int neq = 0;
 #pragma unroll
-  for (int q = 0; q < N; ++q) neq += ok[q] && mono(v[q]) == tau;
-  int eq_before = wave_excl(neq);
+  for (int q = 0; q < N; ++q) neq += ok[q] && key[q] == tau;
+  static_assert(N < 32, "per-lane counts below 2^5");
+  int eq_before = wave_excl_small<5>(neq);
 #pragma unroll
   for (int q = 0; q < N; ++q) {
     in[q] = false;
     if (ok[q]) {
-      const uint32_t k = mono(v[q]);
+      const uint32_t k = key[q];
       if (k > tau) {
         in[q] = true;
       } else if (k == tau) {
@@ -505,14 +527,56 @@ __global__ __launch_bounds__(TK_THR) void k_topk_cand(const float* __restrict__ 
     idx[q] = e0 + q;
   }
   const int kk = min(top_k, V - c * TK_CH);
+  uint32_t key[TK_EPL];
+  uint32_t lmax = 0u;
+  bool lhas = false;
+#pragma unroll
+  for (int q = 0; q < TK_EPL; ++q) {
+    key[q] = mono(v[q]);
+    if (ok[q]) {
+      lmax = max(lmax, key[q]);
+      lhas = true;
+    }
+  }
+  const uint32_t kmax = wave_max_u32(lmax);
+  // lower bound for the chunk's kk-th largest key: the kk-th largest of the
+  // lanes' maxima (kk entries reach it); the entries at or above it are few
+  // for real logits and are searched narrowly, two per lane
+  uint32_t tlo = 0u;
+  if (wave_count(lhas) >= kk) {
+    const uint32_t lk[1] = {lmax};
+    const bool lo1[1] = {lhas};
+    int unused;
+    tlo = wave_kth_key<1>(lk, lo1, kk, 0u, kmax, unused);
+  }
+  int cnt = 0;
+#pragma unroll
+  for (int q = 0; q < TK_EPL; ++q) cnt += ok[q] && key[q] >= tlo;
+  static_assert(TK_EPL < 32, "per-lane counts below 2^5");
+  const int total = wave_sum_small<5>(cnt);
   int ngt;
-  const uint32_t tau = wave_kth_key<TK_EPL>(v, ok, kk, ngt);
+  uint32_t tau;
+  if (total <= TK_NARROW_WAVE) {
+    __shared__ uint32_t cs[TK_THR / 64][TK_NARROW_WAVE];
+    int p = wave_excl_small<5>(cnt);
+#pragma unroll
+    for (int q = 0; q < TK_EPL; ++q)
+      if (ok[q] && key[q] >= tlo) cs[wave][p++] = key[q];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t k2[2] = {cs[wave][lane], cs[wave][lane + 64]};
+    const bool o2[2] = {lane < total, lane + 64 < total};
+    tau = wave_kth_key<2>(k2, o2, kk, tlo, kmax, ngt);
+  } else {
+    tau = wave_kth_key<TK_EPL>(key, ok, kk, 0u, kmax, ngt);
+  }
   bool in[TK_EPL];
-  wave_keep<TK_EPL>(v, ok, idx, tau, kk - ngt, in, nullptr);
+  wave_keep<TK_EPL>(key, ok, idx, tau, kk - ngt, in, nullptr);
   int nin = 0;
 #pragma unroll
   for (int q = 0; q < TK_EPL; ++q) nin += in[q];
-  int pos = wave_excl(nin);
+  int pos = wave_excl_small<5>(nin);
   TkChunk* o = out + (int64_t)r * nch + c;
   float bg = -INFINITY;
   int bgi = 0x7fffffff;
@@ -541,6 +605,7 @@ __global__ __launch_bounds__(TK_THR) void k_topk_cand(const float* __restrict__ 
     o->g = bg;
     o->gi = bgi;
     o->n = kk;
+    o->kmax = kmax;
   }
 }
 
@@ -573,31 +638,94 @@ __device__ __forceinline__ TkRow tk_finish_row(const TkChunk* __restrict__ ch, i
     gv[q] = ok[q] && draw ? ch[cc].gz[j] : 0.f;
   }
   const int kk = min(top_k, V);
-  uint32_t lo = 0u, hi = 0xffffffffu;
-  int it = 0;
-  while (lo < hi) {  // the same sequence in every thread
-    const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
-    int n = 0;
+  uint32_t kz[TK_SPT];
 #pragma unroll
-    for (int q = 0; q < TK_SPT; ++q) n += ok[q] && mono(zv[q]) >= mid;
-    n = wave_isum(n);
-    if (lane == 0) red[it & 1][wave] = n;  // alternating buffers: one barrier per step
-    __syncthreads();
-    int tot = 0;
-#pragma unroll
-    for (int w = 0; w < TK_THR / 64; ++w) tot += red[it & 1][w];
-    if (tot >= kk) lo = mid;
-    else hi = mid - 1u;
-    ++it;
+  for (int q = 0; q < TK_SPT; ++q) kz[q] = mono(zv[q]);
+  // lower bound for the row's kk-th largest key: the kk-th largest of the
+  // chunks' maxima (kk entries reach it), and the row's largest key
+  __shared__ uint32_t bound_sm[2], tau_sm;
+  __shared__ int cnt_sm[TK_THR / 64];
+  __shared__ uint32_t cs[TK_NARROW_ROW];
+  static_assert(TK_NCH <= 64, "one chunk maximum per lane of a wave");
+  if (wave == 0) {
+    const bool has = lane < nch && ch[lane].n > 0;
+    const uint32_t cm[1] = {has ? ch[lane].kmax : 0u};
+    const bool co[1] = {has};
+    const uint32_t rmax = wave_max_u32(cm[0]);
+    uint32_t tlo = 0u;
+    if (wave_count(has) >= kk) {
+      int unused;
+      tlo = wave_kth_key<1>(cm, co, kk, 0u, rmax, unused);
+    }
+    if (lane == 0) {
+      bound_sm[0] = tlo;
+      bound_sm[1] = rmax;
+    }
   }
-  const uint32_t tau = lo;
+  __syncthreads();
+  const uint32_t tlo = bound_sm[0], rmax = bound_sm[1];
+  int cnt = 0;
+#pragma unroll
+  for (int q = 0; q < TK_SPT; ++q) cnt += ok[q] && kz[q] >= tlo;
+  static_assert(TK_SPT < 32, "per-thread counts below 2^5");
+  const int wcnt = wave_sum_small<5>(cnt);
+  if (lane == 0) cnt_sm[wave] = wcnt;
+  __syncthreads();
+  int total = 0, before = 0;
+#pragma unroll
+  for (int w = 0; w < TK_THR / 64; ++w) {
+    total += cnt_sm[w];
+    if (w < wave) before += cnt_sm[w];
+  }
+  uint32_t tau;
+  if (total <= TK_NARROW_ROW) {
+    // the few keys at or above the bound, searched by one wave
+    int p = before + wave_excl_small<5>(cnt);
+#pragma unroll
+    for (int q = 0; q < TK_SPT; ++q)
+      if (ok[q] && kz[q] >= tlo) cs[p++] = kz[q];
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t k4[4];
+      bool o4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        o4[u] = lane + 64 * u < total;
+        k4[u] = o4[u] ? cs[lane + 64 * u] : 0u;
+      }
+      int unused;
+      const uint32_t t = wave_kth_key<4>(k4, o4, kk, tlo, rmax, unused);
+      if (lane == 0) tau_sm = t;
+    }
+    __syncthreads();
+    tau = tau_sm;
+  } else {
+    uint32_t lo = 0u, hi = rmax;
+    int it = 0;
+    while (lo < hi) {  // the same sequence in every thread
+      const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+      int n = 0;
+#pragma unroll
+      for (int q = 0; q < TK_SPT; ++q) n += wave_count(ok[q] && kz[q] >= mid);
+      if (lane == 0) red[it & 1][wave] = n;  // alternating buffers: one barrier per step
+      __syncthreads();
+      int tot = 0;
+#pragma unroll
+      for (int w = 0; w < TK_THR / 64; ++w) tot += red[it & 1][w];
+      if (tot >= kk) lo = mid;
+      else hi = mid - 1u;
+      ++it;
+    }
+    tau = lo;
+  }
   int ngt = 0, neq = 0;
 #pragma unroll
   for (int q = 0; q < TK_SPT; ++q) {
     ngt += ok[q] && mono(zv[q]) > tau;
     neq += ok[q] && mono(zv[q]) == tau;
   }
-  const int wgt = wave_isum(ngt), weq_ex = wave_excl(neq), weq = wave_isum(neq);
+  static_assert(TK_SPT < 32, "per-thread counts below 2^5");
+  const int wgt = wave_sum_small<5>(ngt), weq_ex = wave_excl_small<5>(neq), weq = wave_sum_small<5>(neq);
   __syncthreads();
   if (lane == 0) {
     red[0][wave] = wgt;

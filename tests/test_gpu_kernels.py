@@ -388,6 +388,54 @@ def test_spec_accept_topk_ties_v65536():
         _say(f"top-k ties T={T}: accepted {sum(r[1] for r in recs)} of {B * k}")
 
 
+def _topk_path_rows(V, seed_np=17):
+    """Target logits rows that drive each branch of the chunked top-k passes
+    (k_topk_cand: the lanes' maxima bound a chunk's top-k from below and at
+    most 128 entries at or above it are searched narrowly; k_topk_stats /
+    k_topk_draft: the chunks' maxima bound the row's, at most 256 candidates
+    searched narrowly; more take the search over every entry)."""
+    rng = np.random.default_rng(seed_np)
+    base = lambda: (15 * np.tanh(rng.standard_normal(V) * 2 / 15)).astype(np.float32)  # noqa: E731
+    rows = []
+    rows.append(base())                                    # smooth: narrow everywhere
+    r = base() - 20.0                                      # chunk 3: 2 entries per lane at L = 5 -> exactly
+    for lane in range(64):                                 # 128 at the bound (narrow); the row's top 40 tie at L
+        r[3 * 1024 + 16 * lane: 3 * 1024 + 16 * lane + 2] = 5.0
+    rows.append(r)
+    r = rows[-1].copy()                                    # one more at L: 129 (chunk search over every entry)
+    r[3 * 1024 + 2] = 5.0
+    rows.append(r)
+    r = base()                                             # chunk 5: 200 tied maxima (chunk fallback, row narrow)
+    r[5 * 1024: 5 * 1024 + 200] = 16.0
+    rows.append(r)
+    rows.append(np.full(V, 0.25, np.float32))              # all equal: both passes search every entry
+    rows.append((np.round(base() * 2) / 2).astype(np.float32))  # coarse grid: ties at many cuts
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("V", [65536, 65000])
+def test_spec_accept_topk_search_paths(V):
+    """The top-k accept path (k_topk_cand, k_topk_stats, k_accept) on rows
+    crafted to take the narrow and the full threshold searches of both passes,
+    with ties at the cut, against the oracle's accept_round (flaxchat/engine.py:
+    461-466, 525-592); V = 65000 leaves a 488-entry last chunk with fewer lanes
+    than top_k (no lower bound there). Sampled and greedy."""
+    from oracle import sampling as S
+    _say(f"top-k search paths V={V}")
+    rows = _topk_path_rows(V)
+    B, k, seed, top_k = rows.shape[0], 2, 9, 40
+    rng = np.random.default_rng(3)
+    P = np.stack([np.stack([rows[b]] * (k + 1)) for b in range(B)]).astype(np.float32)
+    P[:, 1:] += (rng.standard_normal((B, k, V)) * 1e-3).astype(np.float32) * (np.arange(B) != 4)[:, None, None]
+    Q = (15 * np.tanh((P[:, :k] + rng.standard_normal((B, k, V)) * 0.5) / 15)).astype(np.float32)
+    rnd = (np.arange(B) % 3).astype(np.int32)
+    for T in (0.8, 0.0):
+        drafts = np.array([[S.draft_sample(Q[b, i], T, top_k, seed, b, int(rnd[b]), i) for i in range(k)]
+                           for b in range(B)], np.int32)
+        recs = _check_accept(P, Q, drafts, rnd, T, top_k, seed)
+        _say(f"  T={T}: accepted {sum(r[1] for r in recs)} of {B * k}")
+
+
 # ---------------------------------------------------------------- attention prologue
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 def test_attn_prologue_vs_oracle(dtype):
