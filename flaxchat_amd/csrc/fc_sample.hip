@@ -1281,10 +1281,22 @@ __global__ __launch_bounds__(VP_THR) void k_accept_decide(SpecDev s, const VPart
   ctl[b] = d;
 }
 
+// Top-k rows (T > 0): the decisions from the finished target row statistics
+// (k_topk_stats), recorded for k_draw_part / k_accept_finish like
+// k_accept_decide's; one thread per row.
+__global__ __launch_bounds__(64) void k_accept_decide_st(SpecDev s, Decision* __restrict__ ctl) {
+  __shared__ Decision d;
+  const int b = blockIdx.x;
+  if (threadIdx.x != 0) return;
+  decide(s, b, s.p_stats + b * (s.k + 1), d);
+  ctl[b] = d;
+}
+
 // Chunk partials of the rejection draw (z = 0, slot 48, from p or from the
 // residual max(0, p - q)) and the bonus draw (z = 1, slot 49, from p) of
-// each row, as requested by k_accept_decide.
-template <int NV>
+// each row, as requested by k_accept_decide (k_accept_decide_st). TOPK: p
+// and q are zero outside the rows' keep sets (the statistics' tau / tie_idx).
+template <int NV, bool TOPK>
 __global__ __launch_bounds__(VP_THR) void k_draw_part(SpecDev s, const Decision* __restrict__ ctl, int vec,
                                                       DPart* __restrict__ out) {
   __shared__ float redv[16];
@@ -1309,6 +1321,7 @@ __global__ __launch_bounds__(VP_THR) void k_draw_part(SpecDev s, const Decision*
   const float* zq = s.q_logits + ((int64_t)b * K + min(row, K - 1)) * V;
   const fc_rowstat qs = s.q_stats[b * K + min(row, K - 1)];
   const int rnd = s.round[b];
+  const uint32_t tp = TOPK ? mono(ps.tau) : 0u, tq = TOPK ? mono(qs.tau) : 0u;
   float bs = -INFINITY, bA = -INFINITY, bg = -INFINITY, R = 0.f;
   int bsi = 0x7fffffff, bAi = 0x7fffffff, bgi = 0x7fffffff;
 #pragma unroll
@@ -1325,10 +1338,13 @@ __global__ __launch_bounds__(VP_THR) void k_draw_part(SpecDev s, const Decision*
       const int i = e + w;
       if (i >= V) break;
       const float G = gumbel_of(pick(rr, w));
-      const float p = expf(vp[w] / T - ps.mx) / ps.sum;
+      float p = expf(vp[w] / T - ps.mx) / ps.sum;
+      if (TOPK && !kept(vp[w], i, tp, ps.tie_idx)) p = 0.f;
       argmax_merge(bs, bsi, logf(fmaxf(p, 1e-10f)) + G, i);
       if (mode == 2) {
-        const float rv = fmaxf(p - expf(vq[w] / T - qs.mx) / qs.sum, 0.f);
+        float pq = expf(vq[w] / T - qs.mx) / qs.sum;
+        if (TOPK && !kept(vq[w], i, tq, qs.tie_idx)) pq = 0.f;
+        const float rv = fmaxf(p - pq, 0.f);
         R += rv;
         if (rv > 0.f) argmax_merge(bA, bAi, logf(rv) + G, i);
         argmax_merge(bg, bgi, G, i);
@@ -1474,25 +1490,41 @@ extern "C" int32_t fc_spec_accept(const fc_spec_state* st, void* stream) {
       rc = fc_launch_row_stats(st->p_logits, B * (K + 1), V, st->temperature, st->top_k, st->p_stats, s);
       if (rc) return rc;
     }
-    hipLaunchKernelGGL(k_accept, dim3(B), dim3(NTHR), 0, s, d);
+    if (!tk_fast(st)) {
+      hipLaunchKernelGGL(k_accept, dim3(B), dim3(NTHR), 0, s, d);
+      FC_LAUNCH_CHECK();
+      return FC_OK;
+    }
+    // decisions from the statistics, the draws split over the vocabulary
+    const PartLayout L = part_layout(st->part, B, K, V);
+    hipLaunchKernelGGL(k_accept_decide_st, dim3(B), dim3(64), 0, s, d, L.ctl);
     FC_LAUNCH_CHECK();
-    return FC_OK;
+  } else {
+    const PartLayout L = part_layout(st->part, B, K, V);
+    int nch = 0;
+    rc = launch_vpart(st->p_logits, V, B * (K + 1), V, st->temperature, false, st->seed, st->round, 0, L.vp, &nch,
+                      s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_accept_decide, dim3(B), dim3(VP_THR), 0, s, d, L.vp, nch, L.ctl);
+    FC_LAUNCH_CHECK();
   }
   const PartLayout L = part_layout(st->part, B, K, V);
-  int nch = 0;
-  rc = launch_vpart(st->p_logits, V, B * (K + 1), V, st->temperature, false, st->seed, st->round, 0, L.vp, &nch, s);
-  if (rc) return rc;
-  hipLaunchKernelGGL(k_accept_decide, dim3(B), dim3(VP_THR), 0, s, d, L.vp, nch, L.ctl);
-  FC_LAUNCH_CHECK();
   const int nv = vp_nv(B, V), dch = vp_nch(V, nv);
   const int vec = (V % 4 == 0) && ((uintptr_t)st->p_logits % 16 == 0) && ((uintptr_t)st->q_logits % 16 == 0);
   const dim3 grid(dch, B, 2);
-  switch (nv) {
-    case 1: hipLaunchKernelGGL(k_draw_part<1>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
-    case 2: hipLaunchKernelGGL(k_draw_part<2>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
-    case 4: hipLaunchKernelGGL(k_draw_part<4>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
-    default: hipLaunchKernelGGL(k_draw_part<8>, grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp); break;
+  const bool tk = !chunked(st);
+#define DRAW_PART(NVV)                                                                                       \
+  {                                                                                                          \
+    if (tk) hipLaunchKernelGGL((k_draw_part<NVV, true>), grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp);      \
+    else hipLaunchKernelGGL((k_draw_part<NVV, false>), grid, dim3(VP_THR), 0, s, d, L.ctl, vec, L.dp);        \
   }
+  switch (nv) {
+    case 1: DRAW_PART(1); break;
+    case 2: DRAW_PART(2); break;
+    case 4: DRAW_PART(4); break;
+    default: DRAW_PART(8); break;
+  }
+#undef DRAW_PART
   FC_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_accept_finish, dim3(B), dim3(64), 0, s, d, L.ctl, L.dp, dch);
   FC_LAUNCH_CHECK();
