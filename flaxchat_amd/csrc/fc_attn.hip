@@ -60,14 +60,24 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
   const int64_t item = (int64_t)blockIdx.x * 4 + wave;
   if (item >= (int64_t)Mcap * NH) return;
   const int m = (int)(item / NH), hh = (int)(item % NH);
-  if (Mdev != nullptr && m >= *Mdev) return;
-  const int b = tok_row[m], pos = tok_pos[m];
-  if ((unsigned)b >= (unsigned)B) return;
   const int half = hd >> 1;
   const bool act = lane < half;
+  const bool vhead = hh >= H + G;
+  // every load that needs neither the token's row nor its position is
+  // issued before any of them is waited for (all lie within the Mcap rows);
+  // the rotary table and the value-embedding row follow as one second batch
+  const int mdev = Mdev != nullptr ? *Mdev : Mcap;
+  const int b = tok_row[m], pos = tok_pos[m];
   const float* row = qkv + ((int64_t)m * NH + hh) * hd;
   float x1 = act ? row[lane] : 0.f, x2 = act ? row[lane + half] : 0.f;
-  if (hh < H + G) {
+  int tok = 0;
+  float part = 0.f;
+  if (vhead && ve != nullptr) {
+    tok = tokens[m];
+    part = lane < 12 ? ld<T>(h, act_idx<T>(m, lane, D)) * ve_gate[(hh - H - G) * 12 + lane] : 0.f;
+  }
+  if (m >= mdev || (unsigned)b >= (unsigned)B) return;
+  if (!vhead) {
     const int pc = min(max(pos, 0), rope_len - 1);
     const float c = act ? rcos[(int64_t)pc * half + lane] : 0.f;
     const float s = act ? rsin[(int64_t)pc * half + lane] : 0.f;
@@ -97,15 +107,16 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
   } else {
     const int g = hh - H - G;
     if (ve != nullptr) {
-      float part = lane < 12 ? ld<T>(h, act_idx<T>(m, lane, D)) * ve_gate[g * 12 + lane] : 0.f;
-      const float z = wave_sum(part);
-      const float gate = 3.f * (1.f / (1.f + expf(-z)));
-      const int tok = tokens[m];
+      float v1 = 0.f, v2 = 0.f;
       if (act) {
         const T* vr = ve + ((int64_t)tok * G + g) * hd;
-        x1 = x1 + gate * ld<T>(vr, lane);
-        x2 = x2 + gate * ld<T>(vr, lane + half);
+        v1 = ld<T>(vr, lane);
+        v2 = ld<T>(vr, lane + half);
       }
+      const float z = wave_sum(part);
+      const float gate = 3.f * (1.f / (1.f + expf(-z)));
+      x1 = x1 + gate * v1;
+      x2 = x2 + gate * v2;
     }
     if (act && pos >= 0 && pos < cap) {
       T* vb = vc + ((((int64_t)b * G + g) * (cap / 32) + pos / 32) * hd) * 32;
