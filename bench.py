@@ -143,28 +143,32 @@ def copy_ceiling(dev, n_bytes=1 << 30, n_rep=5):
     return gbs
 
 
-def read_ceiling(dev, n_bytes=1 << 30, n_rep=5):
+def read_ceiling(dev, n_bytes=1 << 30, n_rep=5, n_buf=1, grids=(1024, 2048, 4096, 8192, 16384)):
     """Measured HBM read ceiling: fc_read_probe (each workgroup streams a
     contiguous share with 16-byte non-temporal loads, nothing written) over
-    `n_bytes`, the best of a few grid sizes, rated by the bytes it reads."""
+    `n_bytes`, the best of a few grid sizes, rated by the bytes it reads.
+    Below the 256 MB Infinity Cache, `n_buf` buffers are read in turn so no
+    launch finds its bytes cached."""
     import torch
     from flaxchat_amd import _lib
-    src = torch.empty(n_bytes, dtype=torch.uint8, device=dev)
+    n_bytes -= n_bytes % 4096
+    srcs = [torch.empty(n_bytes, dtype=torch.uint8, device=dev) for _ in range(n_buf)]
     out = torch.empty(4 * 16384, dtype=torch.int32, device=dev)
     s = torch.cuda.current_stream(dev)
     best = 0.0
-    for wgs in (1024, 2048, 4096, 8192, 16384):
-        run = lambda: _lib.check(_lib.lib().fc_read_probe(src.data_ptr(), n_bytes, out.data_ptr(), wgs,  # noqa: E731
-                                                          s.cuda_stream), "fc_read_probe")
-        run()
+    for wgs in grids:
+        run = lambda i: _lib.check(_lib.lib().fc_read_probe(srcs[i % n_buf].data_ptr(), n_bytes,  # noqa: E731
+                                                            out.data_ptr(), wgs, s.cuda_stream), "fc_read_probe")
+        for i in range(n_buf):
+            run(i)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
-        for _ in range(n_rep):
-            run()
+        for i in range(n_rep * n_buf):
+            run(i)
         e1.record(s)
         e1.synchronize()
-        best = max(best, n_bytes * n_rep / (e0.elapsed_time(e1) / 1e3) / 1e9)
-    del src, out
+        best = max(best, n_bytes * n_rep * n_buf / (e0.elapsed_time(e1) / 1e3) / 1e9)
+    del srcs, out
     return best
 
 
@@ -357,6 +361,9 @@ def main():
         r = attention_roofline(sess)
         ceil = copy_ceiling(target.device)
         rceil = read_ceiling(target.device)
+        # the same probe over one attention launch's bytes: its launch ramp and drain weigh as much
+        rceil_l = read_ceiling(target.device, n_bytes=int(r["per_launch_bytes"]), n_buf=3,
+                               grids=(256, 512, 1024, 2048, 4096))
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
@@ -364,9 +371,12 @@ def main():
                 "per_launch_bytes": int(r["per_launch_bytes"]), "per_launch_us": round(r["per_launch_us"], 2),
                 "S_layer": r["S"], "L_layer": r["L"],
                 "copy_ceiling": round(ceil, 1), "frac_of_copy_ceiling": round(r["achieved"] / ceil, 4),
-                "read_ceiling": round(rceil, 1), "frac_of_read_ceiling": round(r["achieved"] / rceil, 4)}
+                "read_ceiling": round(rceil, 1), "frac_of_read_ceiling": round(r["achieved"] / rceil, 4),
+                "read_ceiling_launch_bytes": round(rceil_l, 1),
+                "frac_of_read_ceiling_launch_bytes": round(r["achieved"] / rceil_l, 4)}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
-              f"1 GiB streaming read: {rceil:.0f} GB/s)", file=sys.stderr, flush=True)
+              f"1 GiB streaming read: {rceil:.0f} GB/s, streaming read of one launch's "
+              f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s)", file=sys.stderr, flush=True)
     topk_line = None
     if not args.no_topk_line and not args.top_k and temp > 0:
         # the same workload with generate_speculative's default top_k=40
