@@ -32,7 +32,25 @@
 #include "fc_common.h"
 #include "fc_internal.h"
 
-template <int EPI>
+// 15 tanh(v / 15) in the bf16 kernels' epilogues. tanh(x) = sign(x) (1 - 2 /
+// (e^{2|x|} + 1)) with e^{2|x|} from the hardware base-2 exponential and the
+// reciprocal from v_rcp_f32 (about 1 ulp each); below |x| = 1/16, where that
+// form cancels, the series x - x^3/3 + 2x^5/15 (truncation < 3e-10). The
+// capped value is within ~5e-6 of 15 tanhf(v / 15), far below the bf16
+// GEMM's own rounding, at about a third of the instructions of the
+// IEEE divide and tanhf. The fp32 kernels keep the exact form.
+__device__ __forceinline__ float softcap15_fast(float v) {
+  const float x = v * (1.f / 15.f);
+  const float a = fabsf(x);
+  const float x2 = x * x;
+  const float ts = x * fmaf(x2, fmaf(x2, 2.f / 15.f, -1.f / 3.f), 1.f);
+  const float ex = __builtin_amdgcn_exp2f(a * 2.8853900817779268f);  // e^{2a}
+  const float tl = copysignf(1.f - 2.f * __builtin_amdgcn_rcpf(ex + 1.f), x);
+  return 15.f * (a < 0.0625f ? ts : tl);
+}
+
+// FAST: the bf16 kernels' softcap (softcap15_fast); the fp32 kernel uses tanhf.
+template <int EPI, bool FAST = false>
 __device__ __forceinline__ void epi_apply(const Epi e, int m, int n, float acc) {
   if constexpr (EPI == EPI_STORE) {
     ((float*)e.out)[(int64_t)m * e.ldo + n] = acc;
@@ -62,7 +80,8 @@ __device__ __forceinline__ void epi_apply(const Epi e, int m, int n, float acc) 
   } else {                                   // EPI_SOFTCAP
     if (n < e.V) {
       const int b = m / e.n_out, rr = m - b * e.n_out;
-      ((float*)e.out)[(int64_t)b * e.row_stride + (int64_t)rr * e.V + n] = 15.f * tanhf(acc / 15.f);
+      ((float*)e.out)[(int64_t)b * e.row_stride + (int64_t)rr * e.V + n] =
+          FAST ? softcap15_fast(acc) : 15.f * tanhf(acc / 15.f);
     }
   }
 }
@@ -374,7 +393,7 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
   Epi ee = e;
   ee.split = s;
 #pragma unroll
-  for (int c = 0; c < OPT; ++c) epi_apply<EPI>(ee, m, n0 + col0 + c, v[c]);
+  for (int c = 0; c < OPT; ++c) epi_apply<EPI, true>(ee, m, n0 + col0 + c, v[c]);
 }
 
 // Attention prologue of one token and one head slot from its fp32 GEMM
@@ -565,7 +584,7 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[M
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = m0 + 16 * mb + 4 * g + i;
-          if (m < M) epi_apply<EPI>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i] * rsc[mb][i]);
+          if (m < M) epi_apply<EPI, true>(ee, m, n0 + 16 * (wave * NBW + j) + r, acc[mb][j][i] * rsc[mb][i]);
         }
   }
 }
@@ -879,8 +898,8 @@ __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0,
   } else if constexpr (EPI == EPI_SOFTCAP) {  // logits row (m / n_out, m % n_out), columns past V dropped
     const int b = m / e.n_out, rr = m - b * e.n_out;
     float* o = (float*)e.out + (int64_t)b * e.row_stride + (int64_t)rr * e.V + n;
-    const float t0 = 15.f * tanhf(v0 / 15.f), t1 = 15.f * tanhf(v1 / 15.f);
-    const float t2 = 15.f * tanhf(v2 / 15.f), t3 = 15.f * tanhf(v3 / 15.f);
+    const float t0 = softcap15_fast(v0), t1 = softcap15_fast(v1);
+    const float t2 = softcap15_fast(v2), t3 = softcap15_fast(v3);
     if (n + 3 < e.V && (((uintptr_t)o) & 15) == 0) {
       *(float4*)o = float4{t0, t1, t2, t3};
     } else {
@@ -890,10 +909,10 @@ __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0,
       if (n + 3 < e.V) o[3] = t3;
     }
   } else {
-    epi_apply<EPI>(e, m, n, v0);
-    epi_apply<EPI>(e, m, n + 1, v1);
-    epi_apply<EPI>(e, m, n + 2, v2);
-    epi_apply<EPI>(e, m, n + 3, v3);
+    epi_apply<EPI, true>(e, m, n, v0);
+    epi_apply<EPI, true>(e, m, n + 1, v1);
+    epi_apply<EPI, true>(e, m, n + 2, v2);
+    epi_apply<EPI, true>(e, m, n + 3, v3);
   }
 }
 template <int EPI, int NB>

@@ -110,6 +110,40 @@ def test_gemm_parity(dtype, M, epi, NK):
     np.testing.assert_allclose(got, ref, rtol=tol, atol=tol * max(1.0, np.abs(ref).max()))
 
 
+@pytest.mark.parametrize("M", [3, 32, 224, 1100, 4100])
+def test_gemm_softcap_range(M):
+    """The bf16 kernels' softcap (exponential / reciprocal form, series below
+    |x| = 1/16) against 15 tanh(z / 15) in float64 over pre-cap values from
+    2^-14 to 2^13 of both signs: z = A[m, 0] W[n, 0] is exact in fp32
+    (bf16 x bf16), so the error is the softcap's alone. Row counts route to
+    the K-split, LDS-shared, 64-row and 256 x 256 tile kernels."""
+    from flaxchat_amd.runtime import frag_pack
+    _say(f"gemm softcap range M={M}")
+    N, K = 4096, 128
+    e = np.arange(M) % 24 - 12                      # 2^-12 .. 2^11
+    s = np.where(np.arange(M) % 2 == 0, 1.0, -1.0) * np.exp2(e)
+    c = ((np.arange(N) % 64) - 32) / 4.0            # -8 .. 7.75 in steps of 1/4
+    A = np.zeros((M, K), np.float32)
+    A[:, 0] = s
+    W = np.zeros((N, K), np.float32)
+    W[:, 0] = c
+    z = s[:, None] * c[None, :]
+    ref = 15 * np.tanh(z / 15)
+    At = torch.from_numpy(frag_pack(A)).to(dev(), torch.bfloat16)
+    Wt = torch.from_numpy(frag_pack(W)).to(dev(), torch.bfloat16)
+    out = torch.zeros(M, N, device=dev(), dtype=torch.float32)
+    check(lib().fc_gemm(At.data_ptr(), Wt.data_ptr(), out.data_ptr(), M, N, K, _lib.FC_BF16, 4, stream()), "gemm")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref)
+    _say(f"  max abs error {err.max():.2e}; max relative error where |z| < 1: "
+         f"{(err / np.maximum(np.abs(ref), 1e-30))[np.abs(z) < 1].max():.2e}")
+    assert err.max() <= 1e-5
+    small = (np.abs(z) < 1) & (z != 0)
+    assert (err[small] / np.abs(ref[small])).max() <= 1e-5
+    assert np.all(got[z == 0] == 0)
+
+
 def test_pack_operand_matches_host_layout():
     """fc_pack_operand reproduces the documented fragment order (host
     restatement frag_pack), including the zero padding rows."""
