@@ -1231,6 +1231,15 @@ struct GemmPlan {
 #ifndef FC_GEMM_DMA
 #define FC_GEMM_DMA 1
 #endif
+// Row counts from which the layer GEMMs below the 256 x 256 kernel take the
+// larger tiles (large-batch verify chunks, e.g. 128 rows x 9 tokens): c_fc
+// on the LDS-shared 128 x 128 tile, the MLP c_proj unsplit on the LDS-ring
+// 64 x 64 tile, the folded-norm attention c_proj on 32 x 64. A sweep of the
+// three shapes at 224 / 448 / 672 / 896 / 1152 rows put the crossover
+// between 672 and 896 rows.
+#ifndef FC_MID_M
+#define FC_MID_M 832
+#endif
 // Tile shape and K split by typical row count, from sweeps on MI355X at the
 // engine's shapes (N = 1536 / 4608 / 6144 / 65536, K = 1536 / 6144).
 static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
@@ -1273,6 +1282,12 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
       p.S = std::min(K > 2048 ? 8 : 3, s_max);
     }
   } else if (can_split) {
+    if (Mtyp >= FC_MID_M && N % 64 == 0 && FC_GEMM_DMA) {  // enough 64 x 64 tiles: no K split
+      p.dma = true;
+      p.mb = 4;
+      p.nb = 1;
+      return p;
+    }
     p.mb = 2;
     p.nb = 4;
     p.S = std::min(3, s_max);
@@ -1299,6 +1314,19 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
   return p;
 }
 
+// c_fc (the ReLU^2 epilogue): from FC_MID_M rows the LDS-shared 128 x 128 tile
+static GemmPlan plan_relu2(int Mtyp, int N, int K, int dtype) {
+  GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
+  if (dtype == FC_BF16 && !p.big && Mtyp >= FC_MID_M && N % 128 == 0) {
+    p = GemmPlan{};
+    p.S = 1;
+    p.la = true;
+    p.mb = 8;
+    p.nb = 2;
+  }
+  return p;
+}
+
 bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
   if (dtype != FC_BF16 || head_dim != 128 || N % 128 != 0 || K % 64 != 0) return false;
   const GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
@@ -1312,7 +1340,7 @@ static GemmPlan plan_fold_add(int Mtyp, int N) {
   GemmPlan p{};
   p.S = 1;
   p.mb = Mtyp <= 16 ? 1 : 2;
-  p.nb = Mtyp <= 16 ? 2 : (Mtyp <= 32 ? 1 : 2);
+  p.nb = Mtyp <= 16 ? 2 : (Mtyp <= 32 ? 1 : (Mtyp < FC_MID_M ? 2 : 4));
   while (p.nb > 1 && N % (16 * p.nb) != 0) p.nb /= 2;
   if (p.nb == 1 && p.mb != 2) p.nb = 2;
   return p;
@@ -1321,7 +1349,7 @@ int fc_gemm_fold_tiles(int Mtyp, int N) { return N / (16 * plan_fold_add(Mtyp, N
 // the consumer (c_fc: N = 4 D, K = D) prefetches FC_RMS_REG tiles per thread
 // with 256 / MT threads per row
 bool fc_gemm_fold_ok(int Mtyp, int D) {
-  const GemmPlan c = plan_gemm(Mtyp, 4 * D, D, FC_BF16, false);
+  const GemmPlan c = plan_relu2(Mtyp, 4 * D, D, FC_BF16);
   return !c.gemv && !c.big && fc_gemm_fold_tiles(Mtyp, D) <= FC_RMS_REG * (256 / (16 * c.mb));
 }
 
@@ -1347,7 +1375,7 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
     return FC_OK;
   }
   const bool can_split = splits != nullptr && gw.part != nullptr;
-  GemmPlan p = plan_gemm(Mtyp, N, K, dtype, can_split);
+  GemmPlan p = e.mode == EPI_RELU2 && !can_split ? plan_relu2(Mtyp, N, K, dtype) : plan_gemm(Mtyp, N, K, dtype, can_split);
   if (e.mode == EPI_ADD && e.xa != nullptr) {
     FC_CHECK_ARG(dtype == FC_BF16 && e.ssq != nullptr && !can_split, "folded-norm GEMM: bf16, ssq, no split");
     p = plan_fold_add(Mtyp, N);

@@ -111,6 +111,26 @@ def test_full_forward_rejects_bad_input(tiny_pair):
         gpt_forward(m, [[1, 2, 3]], [[1, 2]], dtype="fp32")
 
 
+def test_full_forward_bf16_mid_rows():
+    """n_embd 1024 at 6 x 150 tokens (M = 900, a large-batch verify chunk's
+    size, below the 256 x 256 kernel's tile count): c_fc on the LDS-shared
+    128 x 128 tile reading the folded norm, the attention c_proj's folded
+    norm on 32 x 64 tiles, the MLP c_proj (K = 4096) unsplit on the LDS-ring
+    64 x 64 tile with the residual / lambda / backout epilogue."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    _say("full forward bf16 d1024 6 x 150")
+    cfg = GPTConfig(sequence_len=256, vocab_size=1024, n_layer=2, n_head=8, n_kv_head=8, n_embd=1024,
+                    window_pattern="SL", short_window=64)
+    m = GPT.init_normal(cfg, seed=14, std=0.02).perturb_scalars()
+    ids = np.random.default_rng(14).integers(0, cfg.vocab_size, (6, 150))
+    got = gpt_forward(m, ids, dtype="bf16", chunk=150).cpu().numpy()
+    ref = gpt_call(m, ids)
+    err = float(np.abs(got - ref).max())
+    _say(f"  max abs err {err:.3e}")
+    assert err < 2e-2
+
+
 def test_full_forward_bf16_verify_size_split():
     """n_embd 1024 at 8 x 25 tokens (M = 200, a verify-size chunk): the MLP
     c_proj (K = 4096) takes the split-K path (32 x 64 tiles, 3 splits) whose
