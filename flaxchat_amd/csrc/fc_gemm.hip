@@ -536,24 +536,30 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
 // holds rows 16 mb + 4 g + i, column 16 (wave NBW + j) + r of the tile.
 template <int MB, int NBW, int EPI>
 __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[MB][NBW], const RmsPre& rpre,
-                                              QkvPre& qpre, int m0, int n0, int nt, int s, int M, int K) {
+                                              QkvPre (&qpre)[(MB + 1) / 2], int m0, int n0, int nt, int s, int M,
+                                              int K) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   if constexpr (EPI == EPI_QKV) {
-    // the tile is one head (column tile nt = head slot) for 32 tokens: stage
-    // it in LDS, then 8 threads per token finish it (16 dims each: d and
-    // d + 64 of 8 rotary pairs)
-    static_assert(MB == 2 && NBW == 2, "EPI_QKV needs 32 x 128 tiles");
+    // the tile is one head (column tile nt = head slot) for 32 or 64 tokens:
+    // per 32 tokens, stage them in LDS, then 8 threads per token finish them
+    // (16 dims each: d and d + 64 of 8 rotary pairs)
+    static_assert((MB == 2 || MB == 4) && NBW == 2, "EPI_QKV needs 32 x 128 or 64 x 128 tiles");
     __shared__ float T[32][128 + 4];
-    qkv_pre_tab(e.qkv, m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7, qpre);  // in flight while staging
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int p = 0; p < MB / 2; ++p) {
+      const int mt = m0 + 32 * p + (threadIdx.x >> 3);
+      qkv_pre_tab(e.qkv, mt, M, nt, threadIdx.x & 7, qpre[p]);  // in flight while staging
+      if (p > 0) __syncthreads();  // the previous pass's readers are done with T
 #pragma unroll
-      for (int j = 0; j < NBW; ++j)
+      for (int mh = 0; mh < 2; ++mh)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) T[16 * mb + 4 * g + i][16 * (wave * NBW + j) + r] = acc[mb][j][i];
-    __syncthreads();
-    qkv_finish(e.qkv, T[threadIdx.x >> 3], m0 + (threadIdx.x >> 3), M, nt, threadIdx.x & 7, qpre);
+        for (int j = 0; j < NBW; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) T[16 * mh + 4 * g + i][16 * (wave * NBW + j) + r] = acc[2 * p + mh][j][i];
+      __syncthreads();
+      qkv_finish(e.qkv, T[threadIdx.x >> 3], mt, M, nt, threadIdx.x & 7, qpre[p]);
+    }
   } else {
     // folded RMSNorm (RELU2 reading the bf16 copy of x): acc row
     // 16 mb + 4 g + i takes the factor lane 4 g + i computed for its row
@@ -650,8 +656,11 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
   if constexpr (EPI == EPI_RELU2) {
     if (e.rms_in != nullptr) rms_load<16 * MB>(rpre, e, m0, M);
   }
-  QkvPre qpre;  // EPI_QKV: the cache row / position of this thread's token (row m0 + t / 8)
-  if constexpr (EPI == EPI_QKV) qkv_pre_row(e.qkv, m0 + (threadIdx.x >> 3), M, nt, qpre);
+  QkvPre qpre[(MB + 1) / 2];  // EPI_QKV: cache row / position of this thread's token in each 32-row pass
+  if constexpr (EPI == EPI_QKV) {
+#pragma unroll
+    for (int p = 0; p < MB / 2; ++p) qkv_pre_row(e.qkv, m0 + 32 * p + (threadIdx.x >> 3), M, nt, qpre[p]);
+  }
   f32x4 acc[MB][NBW];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -769,7 +778,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
   if constexpr (EPI == EPI_RELU2) {
     if (e.rms_in != nullptr) rms_load<16 * MB>(rpre, e, m0, M);
   }
-  QkvPre qpre;  // unused: the fused QKV epilogue runs on k_gemm_la and k_gemm_big
+  QkvPre qpre[(MB + 1) / 2];  // unused: the fused QKV epilogue runs on k_gemm_la and k_gemm_big
   f32x4 acc[MB][NBW];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -1213,11 +1222,12 @@ static void launch_big(const void* A, const void* W, int Mcap, const int* Mdev, 
 #undef BIG_NB
 }
 
+template <int MB>
 static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
                           hipStream_t s) {
-  const int ntiles = N / 128, mtiles = (Mcap + 31) / 32;
+  const int ntiles = N / 128, mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
   const int nwg = (ntiles + 7) / 8 * 8 * mtiles;
-  hipLaunchKernelGGL((k_gemm_la<2, 2, FC_GEMM_LA_NS, EPI_QKV>), dim3(nwg), dim3(256), 0, s, (const bf16_t*)A,
+  hipLaunchKernelGGL((k_gemm_la<MB, 2, FC_GEMM_LA_NS, EPI_QKV>), dim3(nwg), dim3(256), 0, s, (const bf16_t*)A,
                      (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, 1, mtiles, Mdev == nullptr ? 1 : 0, e);
 }
 
@@ -1233,8 +1243,9 @@ struct GemmPlan {
 #endif
 // Row counts from which the layer GEMMs below the 256 x 256 kernel take the
 // larger tiles (large-batch verify chunks, e.g. 128 rows x 9 tokens): c_fc
-// on the LDS-shared 128 x 128 tile, the MLP c_proj unsplit on the LDS-ring
-// 64 x 64 tile, the folded-norm attention c_proj on 32 x 64. A sweep of the
+// on the LDS-shared 128 x 128 tile, QKV with its fused prologue on 64 x 128,
+// the MLP c_proj unsplit on the LDS-ring 64 x 64 tile, the folded-norm
+// attention c_proj on 32 x 64. A sweep of the
 // three shapes at 224 / 448 / 672 / 896 / 1152 rows put the crossover
 // between 672 and 896 rows.
 #ifndef FC_MID_M
@@ -1330,7 +1341,7 @@ static GemmPlan plan_relu2(int Mtyp, int N, int K, int dtype) {
 bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
   if (dtype != FC_BF16 || head_dim != 128 || N % 128 != 0 || K % 64 != 0) return false;
   const GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
-  // the QKV tile itself is k_gemm_la's 32 x 128, or a 128 x 128 quadrant of k_gemm_big
+  // the QKV tile itself is k_gemm_la's 32 x 128 (64 x 128 from FC_MID_M rows), or a 128 x 128 quadrant of k_gemm_big
   return p.big || p.dma || (p.la && p.mb == 2 && p.nb == 2);
 }
 
@@ -1370,7 +1381,8 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   if (e.mode == EPI_QKV) {
     FC_CHECK_ARG(fc_gemm_fuses_qkv(Mtyp, N, K, dtype, 128), "EPI_QKV needs the 32 x 128 bf16 tile");
     if (plan_gemm(Mtyp, N, K, dtype, false).big) launch_big(A, W, Mcap, Mdev, N, K, e, s);
-    else launch_la_qkv(A, W, Mcap, Mdev, N, K, e, s);
+    else if (Mtyp >= FC_MID_M) launch_la_qkv<4>(A, W, Mcap, Mdev, N, K, e, s);  // 64 x 128 tiles
+    else launch_la_qkv<2>(A, W, Mcap, Mdev, N, K, e, s);
     FC_LAUNCH_CHECK();
     return FC_OK;
   }

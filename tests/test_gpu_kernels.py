@@ -544,11 +544,12 @@ def test_attn_prologue_vs_oracle(dtype):
 
 
 # ---------------------------------------------------------------- fused QKV epilogue
-@pytest.mark.parametrize("H,G,M", [(12, 4, 130), (12, 12, 224), (12, 12, 3400)])
+@pytest.mark.parametrize("H,G,M", [(12, 4, 130), (12, 12, 224), (12, 4, 1000), (12, 12, 3400)])
 def test_attn_qkv_fused_vs_prologue(H, G, M):
     """fc_attn_qkv at verify / prefill row counts runs the attention
     prologue inside the QKV GEMM's epilogue (the 32 x 128 tile of the
-    LDS-shared kernel; at 3400 rows the 256 x 256 tile's quadrants). Its q
+    LDS-shared kernel; its 64 x 128 tile, two 32-token passes, from 832
+    rows; at 3400 rows the 256 x 256 tile's quadrants). Its q
     and the K / V it appends (RoPE, 1.2 * RMSNorm, the value-embedding gate
     on the V heads) must equal fc_gemm's fp32 projection of the same input
     followed by fc_attn_prologue, element by element within 1e-2 relative
