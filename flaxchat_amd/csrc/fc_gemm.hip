@@ -1299,9 +1299,11 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
       p.nb = 1;
       return p;
     }
+    // 33-160 rows (large-batch draft steps): 32 x 32 tiles, 4-way split;
+    // from there (verify chunks) 32 x 64, 3-way
     p.mb = 2;
-    p.nb = 4;
-    p.S = std::min(3, s_max);
+    p.nb = Mtyp <= 160 ? 2 : 4;
+    p.S = std::min(Mtyp <= 160 ? 4 : 3, s_max);
   } else if (Mtyp >= 128 && N % 128 == 0) {
     // verify / prefill rows: a wide output (lm_head) takes the LDS-shared
     // kernel's 128 x 128 tiles; the layer GEMMs the LDS-ring kernel's 64 x 64
