@@ -43,15 +43,21 @@ __device__ __forceinline__ void st8(float* p, const float* v) {
 // columns and walks the row's tokens, with the embedding loads of the next
 // four tokens issued ahead of the dependent arithmetic. Also records the row
 // and position of every packed token for the later per-token kernels.
+//
+// NORM (bf16, at most EMBED_NORM_MAX tokens per row, D <= 2048: one 8-column
+// slice per thread): also the first layer's RMSNorm, h = x * rsqrt(mean(x^2)
+// + 1e-6) in the next GEMM's fragment order, from per-token block sums of
+// the new x kept in registers, which saves that layer's RMSNorm launch.
 #define EMBED_AHEAD 4
-template <typename T>
+#define EMBED_NORM_MAX 8
+template <typename T, bool NORM>
 __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const float* __restrict__ smear_gate,
                                                float smear_lambda, float r0, float a0,
                                                const int* __restrict__ tokens, const int* __restrict__ row_off,
                                                const int* __restrict__ start, int max_per_row, int Mcap, int D,
                                                int cap, float* __restrict__ hist, float* __restrict__ x,
                                                float* __restrict__ x0, int* __restrict__ tok_row,
-                                               int* __restrict__ tok_pos, int full_smear) {
+                                               int* __restrict__ tok_pos, int full_smear, bf16_t* __restrict__ h) {
   __shared__ float sg[EMBED_MAXW], sinv[EMBED_MAXW];
   const int b = blockIdx.x;
   const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
@@ -88,6 +94,66 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
     }
   }
   __syncthreads();
+  if constexpr (NORM) {
+    __shared__ float nred[EMBED_NORM_MAX][4];
+    const int c0 = threadIdx.x * 8;
+    const bool act = c0 < D;
+    float keep[EMBED_NORM_MAX][8], ssj[EMBED_NORM_MAX];
+    float prev[8];
+#pragma unroll
+    for (int j = 0; j < EMBED_NORM_MAX; ++j) ssj[j] = 0.f;
+    if (act) {
+      if (s0 > 0) ld8(hist + ((int64_t)b * cap + s0 - 1) * D + c0, prev);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) prev[i] = 0.f;
+      float ev[EMBED_NORM_MAX][8];
+#pragma unroll
+      for (int j = 0; j < EMBED_NORM_MAX; ++j)
+        if (j < n) ld8(wte + (int64_t)tokens[base + j] * D + c0, ev[j]);
+#pragma unroll
+      for (int j = 0; j < EMBED_NORM_MAX; ++j) {
+        if (j < n) {
+          float xv[8], nv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            nv[i] = ev[j][i] * sinv[j];
+            xv[i] = nv[i] + sg[j] * prev[i];
+            keep[j][i] = r0 * xv[i] + a0 * xv[i];
+            ssj[j] += keep[j][i] * keep[j][i];
+            prev[i] = full_smear ? nv[i] : xv[i];
+          }
+          const int pos = s0 + j;
+          if (pos < cap) st8(hist + ((int64_t)b * cap + pos) * D + c0, prev);
+          const int64_t m = base + j;
+          st8(x0 + m * D + c0, xv);
+          st8(x + m * D + c0, keep[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < EMBED_NORM_MAX; ++j) {
+      const float t = wave_sum(ssj[j]);
+      if (lane == 0) nred[j][wave] = t;
+    }
+    __syncthreads();
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < EMBED_NORM_MAX; ++j) {
+        if (j < n) {
+          const float ss = nred[j][0] + nred[j][1] + nred[j][2] + nred[j][3];
+          const float inv = 1.f / sqrtf(ss / (float)D + 1e-6f);
+          uint4 pk;
+          pk.x = (uint32_t)f2bf(keep[j][0] * inv) | ((uint32_t)f2bf(keep[j][1] * inv) << 16);
+          pk.y = (uint32_t)f2bf(keep[j][2] * inv) | ((uint32_t)f2bf(keep[j][3] * inv) << 16);
+          pk.z = (uint32_t)f2bf(keep[j][4] * inv) | ((uint32_t)f2bf(keep[j][5] * inv) << 16);
+          pk.w = (uint32_t)f2bf(keep[j][6] * inv) | ((uint32_t)f2bf(keep[j][7] * inv) << 16);
+          *(uint4*)(h + frag_idx(base + j, c0, D)) = pk;  // 8 consecutive k: 16 contiguous bytes
+        }
+      }
+    }
+    return;
+  }
   for (int c0 = threadIdx.x * 8; c0 < D; c0 += blockDim.x * 8) {
     float prev[8];
     if (s0 > 0) ld8(hist + ((int64_t)b * cap + s0 - 1) * D + c0, prev);
@@ -323,16 +389,24 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   FC_CHECK_ARG((ch->flags & ~FC_CHUNK_FULL_SMEAR) == 0, "unknown fc_chunk flags");
   const int full_smear = ch->flags & FC_CHUNK_FULL_SMEAR;
 
-  if (dt == FC_BF16)
-    hipLaunchKernelGGL(k_embed<bf16_t>, dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
+  // bf16 chunks of few tokens per row: the embedding kernel also writes the
+  // first layer's RMSNorm output (h), and that layer's RMSNorm launch is skipped
+  const bool embed_norm = dt == FC_BF16 && ch->max_per_row <= EMBED_NORM_MAX && D <= 2048 && D % 8 == 0;
+  if (embed_norm)
+    hipLaunchKernelGGL((k_embed<bf16_t, true>), dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
                        ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
-                       full_smear);
+                       full_smear, (bf16_t*)w.h);
+  else if (dt == FC_BF16)
+    hipLaunchKernelGGL((k_embed<bf16_t, false>), dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
+                       m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
+                       ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
+                       full_smear, nullptr);
   else
-    hipLaunchKernelGGL(k_embed<float>, dim3(B), dim3(256), 0, s, (const float*)m->wte, m->smear_gate,
+    hipLaunchKernelGGL((k_embed<float, false>), dim3(B), dim3(256), 0, s, (const float*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
                        ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
-                       full_smear);
+                       full_smear, nullptr);
   FC_LAUNCH_CHECK();
 
   Pending pend{};
@@ -349,8 +423,10 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   const int backout = m->n_layer / 2;
   for (int l = 0; l < m->n_layer; ++l) {
     const fc_layer& L = m->layers[l];
-    norm(Mcap, 0);
-    FC_LAUNCH_CHECK();
+    if (l > 0 || !embed_norm) {
+      norm(Mcap, 0);
+      FC_LAUNCH_CHECK();
+    }
     Epi e{};
     if (fuse_qkv) {  // the QKV GEMM finishes RoPE / QK-norm / VE gate / KV append itself
       e.mode = EPI_QKV;
