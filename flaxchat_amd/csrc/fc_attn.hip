@@ -872,6 +872,12 @@ int64_t fc_attn_part_bytes(int batch, int max_per_row, int n_head, int n_kv_head
   return fc_align(units * 128 * 4) + fc_align(units * 2 * 4);
 }
 
+// Prefill-width chunks (bf16, head_dim 128, >= FC_ATTN_CHUNK_COLS query
+// columns per row and KV group) take k_attn_pf, which writes no partials.
+static bool attn_uses_pf(int dtype, int hd, int typ_per_row, int H, int G) {
+  return dtype == FC_BF16 && hd == 128 && G > 0 && typ_per_row * (H / G) >= FC_ATTN_CHUNK_COLS;
+}
+
 int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, int B, int max_tokens,
                         int max_per_row, int typ_per_row, int H, int G, int hd, int cap, const int* row_off,
                         const int* start, int window, int max_keys, int dtype, void* part, int64_t part_bytes,
@@ -880,7 +886,7 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
   FC_CHECK_ARG(cap % 32 == 0, "cache capacity must be a multiple of 32");
   FC_CHECK_ARG(max_per_row > 0, "max_per_row");
   const float scale = 1.f / sqrtf((float)hd);
-  if (dtype == FC_BF16 && hd == 128 && typ_per_row * (H / G) >= FC_ATTN_CHUNK_COLS) {
+  if (attn_uses_pf(dtype, hd, typ_per_row, H, G)) {
     FC_CHECK_ARG(B * G <= 65535, "batch * n_kv_head must be <= 65535");
     const int ncolmax = max_per_row * (H / G);
     // prefill-width chunks: 128 query columns per workgroup, 32x32x16 MFMA
@@ -995,6 +1001,14 @@ static int fc_scratch_ptr(hipStream_t stream, void** out) {
   return FC_OK;
 }
 
+// Resolves the scratch address of the stream's GPU ahead of time: fc_graph_begin
+// calls it before capture starts, so a captured fc_attention_noalloc makes no
+// runtime lookup inside the capture.
+int fc_noalloc_prepare(hipStream_t stream) {
+  void* p = nullptr;
+  return fc_scratch_ptr(stream, &p);
+}
+
 extern "C" int64_t fc_attention_noalloc_max_bytes(void) { return FC_NOALLOC_SCRATCH_BYTES; }
 
 extern "C" int32_t fc_attention_noalloc(const void* q, const void* kc, const void* vc, void* y, int32_t batch,
@@ -1004,7 +1018,13 @@ extern "C" int32_t fc_attention_noalloc(const void* q, const void* kc, const voi
   FC_CHECK_ARG(q && kc && vc && y && row_off && start, "null pointer");
   FC_CHECK_ARG(batch > 0 && max_tokens > 0 && max_per_row > 0 && n_head > 0 && n_kv_head > 0, "sizes");
   FC_CHECK_ARG(max_keys > 0 && max_keys <= cap, "max_keys must be in [1, cap]");
-  const int64_t need = fc_attn_part_bytes(batch, max_per_row, n_head, n_kv_head, head_dim, max_keys);
+  FC_CHECK_ARG(n_head % n_kv_head == 0, "n_head must be a multiple of n_kv_head");
+  // the same kernel choice as fc_launch_attention (typical = max_per_row
+  // here): only the split decode kernel (bf16, head_dim 128, below prefill
+  // width) writes partials; the prefill and VALU kernels need none
+  const bool split = dtype == FC_BF16 && head_dim == 128 &&
+                     !attn_uses_pf(dtype, head_dim, max_per_row, n_head, n_kv_head);
+  const int64_t need = split ? fc_attn_part_bytes(batch, max_per_row, n_head, n_kv_head, head_dim, max_keys) : 0;
   if (need > FC_NOALLOC_SCRATCH_BYTES) {
     fc_set_error("fc_attention_noalloc: these sizes need " + std::to_string(need) +
                  " bytes of split-KV partials; the static scratch holds " +

@@ -81,6 +81,9 @@ int fc_launch_attention(const void* q, const void* kc, const void* vc, void* y, 
                         int max_per_row, int typ_per_row, int H, int G, int hd, int cap, const int* row_off,
                         const int* start, int window, int max_keys, int dtype, void* part, int64_t part_bytes,
                         hipStream_t s);
+// fc_attention_noalloc's scratch address for the stream's GPU, looked up now
+// (fc_graph_begin runs it before a capture starts)
+int fc_noalloc_prepare(hipStream_t stream);
 int fc_launch_prologue(const float* qkv, const void* h, const int* tokens, const fc_model* m, int layer,
                        const fc_cache* c, const int* tok_row, const int* tok_pos, int Mcap, const int* Mdev, void* q,
                        hipStream_t s);

@@ -28,6 +28,10 @@ extern "C" const char* fc_last_error(void) { return g_err.c_str(); }
 extern "C" int32_t fc_version(void) { return 100; }
 
 extern "C" int32_t fc_graph_begin(void* stream) {
+  // the allocation-free attention's scratch address is a runtime lookup: done
+  // here, before the capture, so captured calls only read the cached address
+  const int rc = fc_noalloc_prepare((hipStream_t)stream);
+  if (rc != FC_OK) return rc;
   FC_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
   return FC_OK;
 }

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 from typing import List, Optional
 
 import numpy as np
@@ -70,6 +71,18 @@ def default_device() -> torch.device:
 
 _MATS = ("wqkv", "wo", "wfc", "wproj")
 
+# Live DeviceModels by the host address of their fc_model descriptor: callers
+# that hand a model across an integer boundary (the torch operators) resolve
+# it here, so a stale or foreign address is refused instead of dereferenced.
+_LIVE_MODELS: "weakref.WeakValueDictionary[int, DeviceModel]" = weakref.WeakValueDictionary()
+
+
+def live_model(addr: int) -> Optional["DeviceModel"]:
+    """The live DeviceModel whose descriptor is at host address `addr`, or
+    None (never built, or already garbage-collected)."""
+    dm = _LIVE_MODELS.get(int(addr))
+    return dm if dm is not None and ctypes.addressof(dm.desc) == int(addr) else None
+
 
 class DeviceModel:
     """A model's parameters in the engine's HBM layout plus the fc_model
@@ -104,6 +117,7 @@ class DeviceModel:
                             float(self.s["smear_lambda"]), float(self.s["backout_lambda"]),
                             _ptr(self.t["rope_cos"]), _ptr(self.t["rope_sin"]), int(self.t["rope_cos"].shape[0]),
                             ctypes.cast(self._layers, ctypes.POINTER(FcLayer)))
+        _LIVE_MODELS[ctypes.addressof(self.desc)] = self
 
     @staticmethod
     def _rope(config: GPTConfig, device, rope_len: Optional[int] = None):
@@ -147,8 +161,9 @@ class DeviceModel:
                        smear_gate=up(model.smear_gate.kernel.reshape(-1), torch.float32))
         scalars = dict(resid=model.resid_lambdas.tolist(), x0=model.x0_lambdas.tolist(),
                        smear_lambda=float(model.smear_lambda[0]), backout_lambda=float(model.backout_lambda[0]))
-        torch.cuda.synchronize(device)  # engine streams do not order after the default stream
-        return cls(c, code, device, tensors, scalars)
+        if torch.device(device).type == "cuda":
+            torch.cuda.synchronize(device)  # engine streams do not order after the default stream
+        return cls(c, code, torch.device(device), tensors, scalars)
 
     @classmethod
     def random_init(cls, config: GPTConfig, seed: int = 0, dtype="bf16", device=None, std: float = 0.02,

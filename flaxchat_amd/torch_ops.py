@@ -188,22 +188,50 @@ from typing import List, Tuple  # noqa: E402
 SPEC_BUFFERS = list(_lib._SPEC_PTRS) + ["part"]
 
 
-def _model(addr: int) -> "ctypes.pointer":
-    if addr == 0:
-        raise ValueError("model: the address of an fc_model descriptor (DeviceModel.desc)")
-    return ctypes.cast(ctypes.c_void_p(addr), ctypes.POINTER(_lib.FcModel))
+def _model(addr: int):
+    """(descriptor pointer, DeviceModel) of the live DeviceModel whose
+    fc_model descriptor sits at host address `addr`. Any other integer (a
+    stale address of a collected model, a hand-built descriptor) is refused:
+    the kernels would dereference its weight pointers."""
+    from .runtime import live_model
+    dm = live_model(addr) if addr else None
+    if dm is None:
+        raise ValueError("model: the descriptor address of a live DeviceModel (ctypes.addressof(DeviceModel.desc))")
+    return ctypes.pointer(dm.desc), dm
 
 
-def _cache(k_cache: torch.Tensor, v_cache: torch.Tensor, hist: torch.Tensor = None) -> _lib.FcCache:
-    """fc_cache over one model's cache tensors: k [L][B][G][cap][hd],
-    v of as many elements, hist [B][cap][n_embd] fp32 (or absent)."""
-    if k_cache.dim() != 5 or v_cache.numel() != k_cache.numel():
-        raise ValueError("k_cache [layers][batch][kv heads][cap][head_dim] and a v_cache of as many elements")
+def _tdt(dm) -> torch.dtype:
+    return torch.bfloat16 if dm.dtype == _lib.FC_BF16 else torch.float32
+
+
+def _same_device(dm, *ts):
+    """Every tensor on the model's device (meta / fake tensors carry no
+    memory and are checked for shape only)."""
+    for t in ts:
+        if t is not None and t.device.type != "meta" and t.device != dm.device:
+            raise ValueError(f"tensor on {t.device}, the model's weights are on {dm.device}")
+
+
+def _cache(dm, k_cache: torch.Tensor, v_cache: torch.Tensor, hist: torch.Tensor = None) -> _lib.FcCache:
+    """fc_cache over one model's cache tensors, checked against the model:
+    k [n_layer][batch][n_kv_head][cap][head_dim] in the model dtype, v of as
+    many elements, hist [batch][cap][n_embd] fp32 (or absent)."""
+    if k_cache.dim() != 5 or (k_cache.shape[0], k_cache.shape[2], k_cache.shape[4]) != (dm.L, dm.G, dm.hd):
+        raise ValueError(f"k_cache [n_layer={dm.L}][batch][n_kv_head={dm.G}][cap][head_dim={dm.hd}] "
+                         f"(got {tuple(k_cache.shape)})")
+    if v_cache.numel() != k_cache.numel():
+        raise ValueError("v_cache must hold as many elements as k_cache")
+    if k_cache.dtype != _tdt(dm) or v_cache.dtype != _tdt(dm):
+        raise ValueError(f"the caches are {_tdt(dm)} like the model (got {k_cache.dtype} / {v_cache.dtype})")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("the caches must be contiguous")
     B, cap = k_cache.shape[1], k_cache.shape[3]
-    if hist is not None and (hist.dtype != torch.float32 or hist.shape[:2] != (B, cap) or not hist.is_contiguous()):
-        raise ValueError("hist: contiguous fp32 [batch][cap][n_embd]")
+    if B < 1 or cap % 32 != 0:
+        raise ValueError("cache capacity must be a multiple of 32")
+    if hist is not None and (hist.dtype != torch.float32 or tuple(hist.shape) != (B, cap, dm.D)
+                             or not hist.is_contiguous()):
+        raise ValueError(f"hist: contiguous fp32 [batch={B}][cap={cap}][n_embd={dm.D}]")
+    _same_device(dm, k_cache, v_cache, hist)
     return _lib.FcCache(k_cache.data_ptr(), v_cache.data_ptr(), hist.data_ptr() if hist is not None else 0, B, cap)
 
 
@@ -213,17 +241,26 @@ def _i32(*ts):
             raise ValueError("index arrays are contiguous int32 tensors")
 
 
+def _gemm_input(dm, h: torch.Tensor, M: int, name: str):
+    """h: the RMS-normed GEMM input of M tokens: bf16 in fragment order
+    ([round16(M)][n_embd], as the forward writes it) or fp32 row-major."""
+    rows = (M + 15) // 16 * 16 if dm.dtype == _lib.FC_BF16 else M
+    if h.dtype != _tdt(dm) or h.numel() < rows * dm.D or not h.is_contiguous():
+        raise ValueError(f"{name}: h is contiguous {_tdt(dm)} with at least {rows} x {dm.D} elements")
+
+
 @torch.library.custom_op(f"{NS}::forward", mutates_args=("k_cache", "v_cache", "hist", "logits", "workspace"))
 def forward(model: int, k_cache: torch.Tensor, v_cache: torch.Tensor, hist: torch.Tensor, tokens: torch.Tensor,
             row_off: torch.Tensor, start: torch.Tensor, max_per_row: int, n_out: int, logits: torch.Tensor,
             workspace: torch.Tensor, typ_tokens: int = 0, flags: int = 0) -> None:
-    m = _model(model)
-    c = _cache(k_cache, v_cache, hist)
+    m, dm = _model(model)
+    c = _cache(dm, k_cache, v_cache, hist)
     _i32(tokens, row_off, start)
+    _same_device(dm, tokens, row_off, start, logits, workspace)
     B = c.batch
     if row_off.numel() != B + 1 or start.numel() != B:
         raise ValueError("forward: row_off has batch + 1 entries and start batch")
-    V = m.contents.vocab
+    V = dm.V
     if n_out > 0 and (logits.dtype != torch.float32 or logits.numel() < B * n_out * V or not logits.is_contiguous()):
         raise ValueError("forward: logits is contiguous fp32 with at least batch * n_out * vocab elements")
     need = lib().fc_forward_workspace_bytes(m, B, tokens.numel(), max_per_row, typ_tokens)
@@ -241,30 +278,37 @@ def _(model, k_cache, v_cache, hist, tokens, row_off, start, max_per_row, n_out,
     return None
 
 
-def _q_out(model: int, M: int, like: torch.Tensor) -> torch.Tensor:
-    m = _model(model).contents
-    dt = torch.bfloat16 if m.dtype == _lib.FC_BF16 else torch.float32
-    return torch.empty((M, m.n_head, m.head_dim), dtype=dt, device=like.device)
+def _q_out(dm, M: int, like: torch.Tensor) -> torch.Tensor:
+    return torch.empty((M, dm.H, dm.hd), dtype=_tdt(dm), device=like.device)
 
 
 @torch.library.custom_op(f"{NS}::attn_prologue", mutates_args=("k_cache", "v_cache"))
 def attn_prologue(model: int, layer: int, k_cache: torch.Tensor, v_cache: torch.Tensor, qkv: torch.Tensor,
                   h: torch.Tensor, tokens: torch.Tensor, tok_row: torch.Tensor, tok_pos: torch.Tensor) -> torch.Tensor:
     _i32(tokens, tok_row, tok_pos)
+    m, dm = _model(model)
     M = tokens.numel()
-    if qkv.dtype != torch.float32 or qkv.dim() != 2 or qkv.shape[0] < M or not qkv.is_contiguous():
-        raise ValueError("attn_prologue: qkv is contiguous fp32 [M][(H + 2G) * head_dim]")
-    c = _cache(k_cache, v_cache)
-    q = _q_out(model, M, qkv)
-    check(lib().fc_attn_prologue(_model(model), layer, ctypes.byref(c), qkv.data_ptr(), h.data_ptr(),
+    if not 0 <= layer < dm.L:
+        raise ValueError(f"attn_prologue: layer {layer} outside [0, {dm.L})")
+    nqkv = (dm.H + 2 * dm.G) * dm.hd
+    if (qkv.dtype != torch.float32 or qkv.dim() != 2 or qkv.shape[0] < M or qkv.shape[1] != nqkv
+            or not qkv.is_contiguous()):
+        raise ValueError(f"attn_prologue: qkv is contiguous fp32 [M][{nqkv}]")
+    if tok_row.numel() < M or tok_pos.numel() < M:
+        raise ValueError("attn_prologue: tok_row / tok_pos hold one entry per token")
+    _gemm_input(dm, h, M, "attn_prologue")
+    c = _cache(dm, k_cache, v_cache)
+    _same_device(dm, qkv, h, tokens, tok_row, tok_pos)
+    q = _q_out(dm, M, qkv)
+    check(lib().fc_attn_prologue(m, layer, ctypes.byref(c), qkv.data_ptr(), h.data_ptr(),
                                  tokens.data_ptr(), tok_row.data_ptr(), tok_pos.data_ptr(), M, q.data_ptr(),
                                  _stream(qkv)), "fc_attn_prologue")
     return q
 
 
 def _q_fake(model: int, M, like: torch.Tensor, cache: torch.Tensor) -> torch.Tensor:
-    m = _model(model).contents  # the descriptor is host memory: readable while tracing
-    return like.new_empty((M, m.n_head, m.head_dim), dtype=cache.dtype)
+    _, dm = _model(model)  # the descriptor is host memory: readable while tracing
+    return like.new_empty((M, dm.H, dm.hd), dtype=cache.dtype)
 
 
 @attn_prologue.register_fake
@@ -277,9 +321,15 @@ def attn_qkv(model: int, layer: int, k_cache: torch.Tensor, v_cache: torch.Tenso
              tokens: torch.Tensor, tok_row: torch.Tensor, tok_pos: torch.Tensor, typ_tokens: int = 0) -> torch.Tensor:
     _i32(tokens, tok_row, tok_pos)
     M = tokens.numel()
-    m = _model(model)
-    c = _cache(k_cache, v_cache)
-    q = _q_out(model, M, h)
+    m, dm = _model(model)
+    if not 0 <= layer < dm.L:
+        raise ValueError(f"attn_qkv: layer {layer} outside [0, {dm.L})")
+    if tok_row.numel() < M or tok_pos.numel() < M:
+        raise ValueError("attn_qkv: tok_row / tok_pos hold one entry per token")
+    _gemm_input(dm, h, M, "attn_qkv")
+    c = _cache(dm, k_cache, v_cache)
+    _same_device(dm, h, tokens, tok_row, tok_pos)
+    q = _q_out(dm, M, h)
     need = lib().fc_attn_qkv_workspace_bytes(m, M, typ_tokens)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device=h.device)
     check(lib().fc_attn_qkv(m, layer, ctypes.byref(c), h.data_ptr(), tokens.data_ptr(), tok_row.data_ptr(),
@@ -315,12 +365,39 @@ def _(logits, temperature, top_k):
     return f(), f(), f(), i(), i()
 
 
-def _spec_state(buffers: List[torch.Tensor], batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed):
+_PMAX, _RES_STRIDE, _ROWSTAT = 16, 40, ctypes.sizeof(_lib.FcRowstat)
+
+
+def _spec_bytes(batch: int, k: int, gen_cap: int, vocab: int) -> dict:
+    """Bytes each fc_spec_state array needs (include/flaxchat_amd.h)."""
+    B = batch
+    n = dict(t_len=B, d_len=B, t_pend=B * _PMAX, d_pend=B * _PMAX, t_pend_n=B, d_pend_n=B, t_dirty=B, d_dirty=B,
+             gen=B * gen_cap, gen_n=B, prompt_len=B, round=B, stall=B, result=B * _RES_STRIDE, tok_d0=B * _PMAX,
+             off_d0=B + 1, start_d=k * B, tok_ds=k * B, off_ds=B + 1, tok_v=B * (_PMAX + k), off_v=B + 1,
+             start_v=B, drafts=B * k, q_logits=B * k * vocab, p_logits=B * (k + 1) * vocab)
+    out = {name: 4 * v for name, v in n.items()}
+    out["q_stats"] = B * k * _ROWSTAT
+    out["p_stats"] = B * (k + 1) * _ROWSTAT
+    out["part"] = int(lib().fc_spec_part_bytes(B, k, vocab))
+    return out
+
+
+def _spec_state(buffers: List[torch.Tensor], batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed,
+                device=None):
     if len(buffers) != len(SPEC_BUFFERS):
         raise ValueError(f"buffers: the {len(SPEC_BUFFERS)} arrays of SPEC_BUFFERS in order")
+    if batch < 1 or k < 1 or vocab < 1 or gen_cap < 1:
+        raise ValueError("batch, k, gen_cap and vocab must be positive")
+    need = _spec_bytes(batch, k, gen_cap, vocab)
+    dev = device if device is not None else buffers[0].device
     for name, t in zip(SPEC_BUFFERS, buffers):
         if not t.is_contiguous():
             raise ValueError(f"buffer {name} must be contiguous")
+        if t.numel() * t.element_size() < need[name]:
+            raise ValueError(f"buffer {name}: {t.numel() * t.element_size()} bytes, {need[name]} needed "
+                             f"for batch {batch}, k {k}, gen_cap {gen_cap}, vocab {vocab}")
+        if t.device != dev:
+            raise ValueError(f"buffer {name} is on {t.device}, not {dev}")
     part = buffers[-1]
     return _lib.FcSpecState(batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed,
                             *[t.data_ptr() for t in buffers[:-1]], part.data_ptr(), part.numel())
@@ -329,6 +406,8 @@ def _spec_state(buffers: List[torch.Tensor], batch, k, max_tokens, gen_cap, voca
 @torch.library.custom_op(f"{NS}::spec_accept", mutates_args=("buffers",))
 def spec_accept(buffers: List[torch.Tensor], batch: int, k: int, max_tokens: int, gen_cap: int, vocab: int,
                 temperature: float, top_k: int, seed: int) -> None:
+    if buffers and buffers[0].device.type != "cuda":
+        raise ValueError("spec_accept: the state buffers live on a CUDA device")
     st = _spec_state(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed)
     check(lib().fc_spec_accept(ctypes.byref(st), _stream(buffers[0])), "fc_spec_accept")
 
@@ -344,9 +423,16 @@ def spec_round(target: int, draft: int, t_k: torch.Tensor, t_v: torch.Tensor, t_
                d_k: torch.Tensor, d_v: torch.Tensor, d_hist: torch.Tensor, buffers: List[torch.Tensor], batch: int,
                k: int, max_tokens: int, gen_cap: int, vocab: int, temperature: float, top_k: int, seed: int,
                workspace: torch.Tensor) -> None:
-    mt, md = _model(target), _model(draft)
-    tc, dc = _cache(t_k, t_v, t_hist), _cache(d_k, d_v, d_hist)
-    st = _spec_state(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed)
+    (mt, tdm), (md, ddm) = _model(target), _model(draft)
+    if tdm.V != vocab or ddm.V != vocab:
+        raise ValueError(f"spec_round: vocab {vocab}, the models have {tdm.V} / {ddm.V}")
+    if tdm.device != ddm.device:
+        raise ValueError("spec_round: target and draft on different devices")
+    tc, dc = _cache(tdm, t_k, t_v, t_hist), _cache(ddm, d_k, d_v, d_hist)
+    if tc.batch != batch or dc.batch != batch:
+        raise ValueError(f"spec_round: the caches hold {tc.batch} / {dc.batch} rows, batch is {batch}")
+    _same_device(tdm, workspace)
+    st = _spec_state(buffers, batch, k, max_tokens, gen_cap, vocab, temperature, top_k, seed, device=tdm.device)
     need = lib().fc_spec_workspace_bytes(mt, md, batch, k)
     if need < 0 or workspace.numel() < need:
         raise ValueError(f"spec_round: workspace of {workspace.numel()} bytes, {need} needed")

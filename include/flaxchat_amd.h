@@ -221,9 +221,13 @@ int32_t fc_attention(const void* q, const void* kc, const void* vc, void* y,
  * ends. No counterpart in the reference: for callers that cannot allocate
  * (code under stream capture, serving loops, harnesses that forbid
  * hipMalloc). Same arguments and result as fc_attention; sizes whose
- * partials (fc_attention_workspace_bytes) exceed the array return
- * FC_ERR_CAPACITY before anything is launched. Every call on one GPU shares
- * that GPU's array: calls that overlap in time on one GPU race. */
+ * partials (fc_attention_workspace_bytes; none for fp32, nor at prefill
+ * width: bf16 head_dim 128 with >= 128 query columns per row and KV group) exceed the
+ * array return FC_ERR_CAPACITY before anything is launched. Every call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU race.
+ * The array's device address is looked up once per GPU, at the first call
+ * or at fc_graph_begin on a stream of that GPU: a caller that captures with
+ * its own hipStreamBeginCapture makes one uncaptured call first. */
 int64_t fc_attention_noalloc_max_bytes(void);
 int32_t fc_attention_noalloc(const void* q, const void* kc, const void* vc, void* y,
                              int32_t batch, int32_t max_tokens, int32_t max_per_row, int32_t n_head,

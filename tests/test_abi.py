@@ -54,6 +54,24 @@ def test_argument_errors_are_status_codes():
     assert L.fc_attn_qkv(ctypes.byref(m), 0, ctypes.byref(c), None, None, None, None, 1, 0, None, None, 0, None) == -1
 
 
+def test_noalloc_refuses_sizes_beyond_scratch():
+    """Sizes whose split-KV partials exceed the static scratch are refused
+    with FC_ERR_CAPACITY before any HIP call, so non-null dummy addresses are
+    never dereferenced (and a regression returns an error here instead of
+    launching over them on a GPU)."""
+    L = _lib.lib()
+    cap_bytes = L.fc_attention_noalloc_max_bytes()
+    assert cap_bytes > 0
+    # 4096 rows x 16 KV groups x 64-token chunks (64 query columns per group:
+    # the split decode kernel, not the prefill one) need far more partials
+    need = L.fc_attention_workspace_bytes(4096, 64, 16, 16, 128, 8192)
+    assert need > cap_bytes
+    p = 0x1000
+    rc = L.fc_attention_noalloc(p, p, p, p, 4096, 4096 * 64, 64, 16, 16, 128, 8192, p, p, 0, 8192, _lib.FC_BF16,
+                                None)
+    assert rc == -4 and b"scratch" in L.fc_last_error()
+
+
 def test_struct_layout_matches_c(tmp_path):
     """Compile a C probe against the header and compare sizes and offsets."""
     fields = {

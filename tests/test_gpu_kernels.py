@@ -354,7 +354,10 @@ def test_spec_accept_cfg3_vs_oracle(T, top_k):
     the same logits, drafts and Philox counters. Without top-k the
     vocab-wide passes run in 64 chunks per row and merge their partials;
     with top_k 40 (generate_speculative's default, engine.py:411, 461-466)
-    one workgroup per row finds the keep set by radix select. Target logits
+    each 1024-entry chunk keeps its exact top-k candidates (k_topk_cand),
+    one workgroup per row selects the keep set among them (k_topk_stats),
+    and the accept decision and its draws run split over the vocabulary as
+    without top-k (k_accept_decide_st, k_draw_part). Target logits
     are 15 tanh(N(0, 2^2) / 15), the draft's the target's plus N(0, 0.5^2)
     noise (softcapped again); drafts are the oracle's own draws from the
     draft logits. The emitted tokens must match exactly."""
@@ -544,6 +547,61 @@ def test_attn_prologue_vs_oracle(dtype):
 
 
 # ---------------------------------------------------------------- fused QKV epilogue
+@pytest.mark.parametrize("dtype,M", [("fp32", 40), ("bf16", 40), ("bf16", 13)])
+def test_attn_qkv_unfused_fallback(dtype, M):
+    """fc_attn_qkv below the fused-epilogue row counts (bf16 with 13 or 40
+    tokens) and for fp32 models takes the unfused path: the QKV GEMM into
+    the caller's workspace, then the prologue kernel. Its q, K and V must
+    equal fc_gemm followed by fc_attn_prologue on the same inputs exactly
+    (the same kernels with the same plan), GQA 12 / 4 with a value-embedding
+    layer and one without, including a skipped token (row -1) and one at
+    position cap."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    from flaxchat_amd.runtime import DeviceCache, DeviceModel
+    from flaxchat_amd.torch_ops import pack_operand
+    _say(f"unfused attn_qkv dtype={dtype} M={M}")
+    D, V, d, H, G = 1536, 4096, 128, 12, 4
+    cfg = GPTConfig(sequence_len=1024, vocab_size=V, n_layer=2, n_head=H, n_kv_head=G, n_embd=D,
+                    window_pattern="SL", short_window=256)
+    dm = DeviceModel.from_host(GPT.init_normal_parallel(cfg, seed=11, std=0.05), dtype=dtype, device=dev())
+    B, cap = 3, 256
+    rng = np.random.default_rng(M + (7 if dtype == "fp32" else 0))
+    slots = rng.permutation(B * cap)[:M]
+    rows, pos = (slots // cap).astype(np.int32), (slots % cap).astype(np.int32)
+    rows[3] = -1
+    pos[5] = cap
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev())  # noqa: E731
+    tok_t, row_t, pos_t = i32(rng.integers(0, V, M)), i32(rows), i32(pos)
+    hrows = torch.from_numpy(rng.standard_normal((M, D)).astype(np.float32)).to(dev())
+    h = pack_operand(hrows.to(torch.bfloat16)) if dtype == "bf16" else hrows.contiguous()
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    code = _lib.FC_BF16 if dtype == "bf16" else _lib.FC_F32
+    NQKV = (H + 2 * G) * d
+    L = _lib.lib()
+    for layer in range(2):
+        ca, cb = DeviceCache(dm, B, cap), DeviceCache(dm, B, cap)
+        qa = torch.zeros(M, H, d, dtype=tdt, device=dev())
+        qb = torch.zeros_like(qa)
+        need = L.fc_attn_qkv_workspace_bytes(ctypes.byref(dm.desc), M, M)
+        assert need >= M * NQKV * 4, "this case should take the unfused path"
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev())
+        check(L.fc_attn_qkv(ctypes.byref(dm.desc), layer, ctypes.byref(ca.desc), h.data_ptr(), tok_t.data_ptr(),
+                            row_t.data_ptr(), pos_t.data_ptr(), M, M, qa.data_ptr(), ws.data_ptr(), ws.numel(),
+                            stream()), "attn_qkv")
+        qkv = torch.zeros(M, NQKV, dtype=torch.float32, device=dev())
+        check(L.fc_gemm(h.data_ptr(), dm.t["layers"][layer]["wqkv"].data_ptr(), qkv.data_ptr(), M, NQKV, D, code, 0,
+                        stream()), "gemm")
+        check(L.fc_attn_prologue(ctypes.byref(dm.desc), layer, ctypes.byref(cb.desc), qkv.data_ptr(), h.data_ptr(),
+                                 tok_t.data_ptr(), row_t.data_ptr(), pos_t.data_ptr(), M, qb.data_ptr(), stream()),
+              "prologue")
+        torch.cuda.synchronize()
+        for name, a, b in (("q", qa, qb), ("k", ca.k[layer], cb.k[layer]), ("v", ca.v[layer], cb.v[layer])):
+            assert b.float().abs().max().item() > 0, f"layer {layer} {name}: reference is all zero"
+            assert torch.equal(a, b), f"layer {layer} {name}: differs from fc_gemm + fc_attn_prologue"
+        assert qa[3].float().abs().sum().item() == 0, "the skipped token wrote q"
+
+
 @pytest.mark.parametrize("H,G,M", [(12, 4, 130), (12, 12, 224), (12, 4, 1000), (12, 12, 3400)])
 def test_attn_qkv_fused_vs_prologue(H, G, M):
     """fc_attn_qkv at verify / prefill row counts runs the attention

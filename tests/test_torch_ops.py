@@ -41,21 +41,105 @@ def test_frag_to_rows_inverts_frag_pack(R, K):
     np.testing.assert_array_equal(ops.frag_to_rows(packed, R).numpy(), a)
 
 
+def _cpu_model(**kw):
+    """An fp32 DeviceModel whose weights sit in host memory: enough for the
+    operators' host-side checks and fake implementations (no kernel runs)."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    from flaxchat_amd.runtime import DeviceModel
+    cfg = GPTConfig(sequence_len=64, vocab_size=256, n_layer=2, n_head=6, n_kv_head=2, n_embd=768,
+                    window_pattern="SL", short_window=32)
+    cfg.__dict__.update(kw)
+    return DeviceModel.from_host(GPT.init_normal(cfg, seed=0, std=0.02), dtype="fp32", device=torch.device("cpu"))
+
+
 def test_engine_op_fakes():
     """Shape propagation of the engine operators on meta tensors (the model
     descriptor is host memory; nothing is launched)."""
     import ctypes
-    from flaxchat_amd import _lib
-    m = _lib.FcModel()
-    m.n_head, m.head_dim, m.dtype = 6, 128, _lib.FC_BF16
-    addr = ctypes.addressof(m)
+    dm = _cpu_model()
+    addr = ctypes.addressof(dm.desc)
     meta = dict(device="meta")
-    kc = torch.empty(2, 3, 2, 64, 128, dtype=torch.bfloat16, **meta)
+    kc = torch.empty(2, 3, 2, 64, 128, **meta)
     i = torch.empty(9, dtype=torch.int32, **meta)
-    h = torch.empty(16, 768, dtype=torch.bfloat16, **meta)
+    h = torch.empty(9, 768, **meta)
     q = torch.ops.flaxchat_mi355x.attn_qkv(addr, 0, kc, kc, h, i, i, i, 0)
-    assert q.shape == (9, 6, 128) and q.dtype == torch.bfloat16
+    assert q.shape == (9, 6, 128) and q.dtype == torch.float32
     qkv = torch.empty(9, 1280, **meta)
     assert torch.ops.flaxchat_mi355x.attn_prologue(addr, 1, kc, kc, qkv, h, i, i, i).shape == (9, 6, 128)
     mx, s, tau, tie, am = torch.ops.flaxchat_mi355x.row_stats(torch.empty(5, 100, **meta), 1.0, 0)
     assert mx.shape == (5,) and am.dtype == torch.int32
+
+
+def test_engine_ops_refuse_foreign_and_stale_descriptors():
+    """Only the descriptor of a live DeviceModel is accepted: a hand-built
+    fc_model, an arbitrary integer and the address of a collected model are
+    refused with ValueError before any pointer reaches the library."""
+    import ctypes
+    import gc
+    from flaxchat_amd import _lib
+    kc = torch.zeros(2, 3, 2, 64, 128)
+    i = torch.zeros(9, dtype=torch.int32)
+    h = torch.zeros(9, 768)
+    raw = _lib.FcModel()
+    raw.n_layer, raw.n_head, raw.head_dim, raw.n_kv_head = 2, 6, 128, 2
+    for addr in (ctypes.addressof(raw), 0x7F0000001000, 0):
+        with pytest.raises(ValueError, match="live DeviceModel"):
+            torch.ops.flaxchat_mi355x.attn_qkv(addr, 0, kc, kc, h, i, i, i, 0)
+    dm = _cpu_model()
+    addr = ctypes.addressof(dm.desc)
+    del dm
+    gc.collect()
+    with pytest.raises(ValueError, match="live DeviceModel"):
+        torch.ops.flaxchat_mi355x.attn_qkv(addr, 0, kc, kc, h, i, i, i, 0)
+
+
+def test_engine_ops_check_tensors_against_the_model():
+    """Each mismatch between a tensor and the model descriptor raises
+    ValueError on the host: cache layers, KV heads, head_dim, dtype and
+    capacity, the GEMM input's size and dtype, the layer index, and every
+    speculative-state buffer's size."""
+    import ctypes
+    dm = _cpu_model()
+    addr = ctypes.addressof(dm.desc)
+    op = torch.ops.flaxchat_mi355x
+    i = torch.zeros(9, dtype=torch.int32)
+    h = torch.zeros(9, 768)
+    good = torch.zeros(2, 3, 2, 64, 128)
+    bad_caches = {
+        "n_layer": torch.zeros(1, 3, 2, 64, 128),
+        "n_kv_head": torch.zeros(2, 3, 6, 64, 128),
+        "head_dim": torch.zeros(2, 3, 2, 64, 64),
+        "dtype": torch.zeros(2, 3, 2, 64, 128, dtype=torch.bfloat16),
+        "cap": torch.zeros(2, 3, 2, 40, 128),
+    }
+    for what, kc in bad_caches.items():
+        with pytest.raises(ValueError):
+            op.attn_qkv(addr, 0, kc, kc, h, i, i, i, 0)
+    with pytest.raises(ValueError):  # v_cache of a different size
+        op.attn_qkv(addr, 0, good, good[:, :2].contiguous(), h, i, i, i, 0)
+    with pytest.raises(ValueError):  # h holds fewer than 9 x 768 values
+        op.attn_qkv(addr, 0, good, good, torch.zeros(8, 768), i, i, i, 0)
+    with pytest.raises(ValueError):  # h in the wrong dtype
+        op.attn_qkv(addr, 0, good, good, h.to(torch.bfloat16), i, i, i, 0)
+    with pytest.raises(ValueError):  # layer past the model
+        op.attn_qkv(addr, 2, good, good, h, i, i, i, 0)
+    with pytest.raises(ValueError):  # qkv of the wrong width
+        op.attn_prologue(addr, 0, good, good, torch.zeros(9, 1024), h, i, i, i)
+    with pytest.raises(ValueError):  # hist of the wrong width
+        op.forward(addr, good, good, torch.zeros(3, 64, 512), i, torch.zeros(4, dtype=torch.int32),
+                   torch.zeros(3, dtype=torch.int32), 3, 0, torch.zeros(1), torch.zeros(1, dtype=torch.uint8))
+    # speculative state: one buffer short of its size for batch 3, k 4, vocab 256
+    from flaxchat_amd.torch_ops import SPEC_BUFFERS, _spec_bytes
+    need = _spec_bytes(3, 4, 100, 256)
+    bufs = [torch.zeros(max(need[n], 1), dtype=torch.uint8) for n in SPEC_BUFFERS]
+    hist = torch.zeros(3, 64, 768)
+    for short in ("gen", "p_logits", "q_stats", "part"):
+        b = list(bufs)
+        b[SPEC_BUFFERS.index(short)] = torch.zeros(max(need[short] - 4, 1), dtype=torch.uint8)
+        with pytest.raises(ValueError, match=short):
+            op.spec_round(addr, addr, good, good, hist, good, good, hist, b, 3, 4, 100, 100, 256, 1.0, 0, 1,
+                          torch.zeros(1, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="vocab"):
+        op.spec_round(addr, addr, good, good, hist, good, good, hist, bufs, 3, 4, 100, 100, 512, 1.0, 0, 1,
+                      torch.zeros(1, dtype=torch.uint8))

@@ -5,6 +5,7 @@ on the same inputs (same kernels, so bit-identical output), on two calls in
 a row where the second is smaller, and a size beyond the scratch is refused
 before anything is launched."""
 
+import ctypes
 import sys
 
 import numpy as np
@@ -79,15 +80,52 @@ def test_noalloc_matches_workspace_entry_point(dtype):
         assert torch.equal(got, ref), f"call {i}: differs from fc_attention"
 
 
-def test_noalloc_refuses_sizes_beyond_scratch():
-    f = _fn()
-    cap_bytes = lib().fc_attention_noalloc_max_bytes()
-    assert cap_bytes > 0
-    # 4096 rows x 16 KV groups x 64-token chunks needs far more partials
-    need = lib().fc_attention_workspace_bytes(4096, 64, 16, 16, 128, 8192)
-    assert need > cap_bytes
-    dummy = torch.zeros(16, dtype=torch.int32, device="cuda")
-    p = dummy.data_ptr()
-    rc = f(p, p, p, p, 4096, 4096 * 64, 64, 16, 16, 128, 8192, p, p, 0, 8192, _lib.FC_BF16,
-           torch.cuda.current_stream().cuda_stream)
-    assert rc == -4 and b"scratch" in lib().fc_last_error()
+def test_noalloc_prefill_width_needs_no_scratch():
+    """bf16 chunks of >= 128 query columns per row and KV group take the
+    prefill kernel, which writes no partials: the allocation-free entry point
+    runs them whatever their size and matches fc_attention bit for bit, and a
+    smaller decode-width call after it still matches."""
+    L = lib()
+    # 4 rows x 1024 tokens x 12 heads: fc_attention_workspace_bytes reports
+    # the decode kernel's partials (far above the scratch), none are needed
+    need = L.fc_attention_workspace_bytes(4, 1024, 12, 12, 128, 2048)
+    assert need > L.fc_attention_noalloc_max_bytes()
+    for i, shape in enumerate([(4, 1024, 12, 12, 0, 1100), (3, 7, 12, 4, 256, 900)]):
+        _say(f"noalloc attention prefill-width call {i} shape={shape}")
+        c = _case(300 + i, *shape, _lib.FC_BF16)
+        ref = _run(c, noalloc=False)
+        got = _run(c, noalloc=True)
+        assert torch.equal(got, ref), f"call {i}: differs from fc_attention"
+
+
+def test_noalloc_under_graph_capture():
+    """fc_attention_noalloc recorded into a graph between fc_graph_begin and
+    fc_graph_end (which looks the scratch address up before the capture),
+    replayed three times with eager work and synchronisations between the
+    replays: every replay equals the eager fc_attention output."""
+    L = lib()
+    c = _case(400, 6, 7, 12, 4, 0, 1300, _lib.FC_BF16)
+    ref = _run(c, noalloc=False)
+    dev = torch.device("cuda", 0)
+    side = torch.cuda.Stream(device=dev)
+    y = torch.full((c["rows"], c["H"] * c["d"]), 3.0, device=dev, dtype=c["tdt"])
+    args = (c["q"].data_ptr(), c["K"].data_ptr(), c["V"].data_ptr(), y.data_ptr(), c["B"], c["tot"], c["W"], c["H"],
+            c["G"], c["d"], c["cap"], c["ro"].data_ptr(), c["st"].data_ptr(), c["window"], c["max_keys"], c["code"])
+    torch.cuda.synchronize()
+    _say("noalloc attention: capture")
+    ex = ctypes.c_void_p()
+    check(L.fc_graph_begin(side.cuda_stream), "fc_graph_begin")
+    rc = L.fc_attention_noalloc(*args, side.cuda_stream)
+    check(L.fc_graph_end(side.cuda_stream, ctypes.byref(ex)), "fc_graph_end")
+    check(rc, "fc_attention_noalloc (captured)")
+    try:
+        for rep in range(3):
+            _say(f"noalloc attention: replay {rep}")
+            y.fill_(3.0)  # the value fc_attention's output buffer started from (padding rows keep it)
+            torch.cuda.synchronize()
+            check(L.fc_graph_launch(ex, side.cuda_stream), "fc_graph_launch")
+            side.synchronize()
+            assert torch.equal(y, ref), f"replay {rep} differs from fc_attention"
+            _run(_case(500 + rep, 2, 3, 6, 6, 0, 400, _lib.FC_BF16), noalloc=False)  # eager work in between
+    finally:
+        L.fc_graph_destroy(ex)
