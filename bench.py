@@ -172,6 +172,33 @@ def read_ceiling(dev, n_bytes=1 << 30, n_rep=5, n_buf=1, grids=(1024, 2048, 4096
     return best
 
 
+def l2_ceiling(dev, region=1 << 20, n_bytes=1 << 30, n_rep=5, grids=(256, 512, 1024)):
+    """Measured L2-to-CU read ceiling: fc_l2_read_probe (each XCD's workgroups
+    read a 1 MB region that stays in that XCD's L2, direct-to-LDS loads)
+    over `n_bytes`, per grid size (256 = one workgroup per CU, the occupancy
+    of the verify GEMMs): {workgroups: GB/s}."""
+    import torch
+    from flaxchat_amd import _lib
+    src = torch.ones(8 * region, dtype=torch.uint8, device=dev)
+    out = torch.empty(4 * max(grids), dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev)
+    res = {}
+    for wgs in grids:
+        per = n_bytes // wgs // 65536 * 65536
+        run = lambda: _lib.check(_lib.lib().fc_l2_read_probe(src.data_ptr(), region, n_bytes, out.data_ptr(),  # noqa: E731
+                                                             wgs, s.cuda_stream), "fc_l2_read_probe")
+        run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(n_rep):
+            run()
+        e1.record(s)
+        e1.synchronize()
+        res[wgs] = round(per * wgs * n_rep / (e0.elapsed_time(e1) / 1e3) / 1e9, 1)
+    del src, out
+    return res
+
+
 def gemm_calibration(n_iter=20, n_copies=4):
     """fc_gemm (fragment-order operands, store epilogue) against torch.matmul
     (hipBLASLt) on the cfg4 engine's GEMM shapes; `n_copies` weight copies are
@@ -364,6 +391,7 @@ def main():
         # the same probe over one attention launch's bytes: its launch ramp and drain weigh as much
         rceil_l = read_ceiling(target.device, n_bytes=int(r["per_launch_bytes"]), n_buf=3,
                                grids=(256, 512, 1024, 2048, 4096))
+        l2c = l2_ceiling(target.device)
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
@@ -373,10 +401,12 @@ def main():
                 "copy_ceiling": round(ceil, 1), "frac_of_copy_ceiling": round(r["achieved"] / ceil, 4),
                 "read_ceiling": round(rceil, 1), "frac_of_read_ceiling": round(r["achieved"] / rceil, 4),
                 "read_ceiling_launch_bytes": round(rceil_l, 1),
-                "frac_of_read_ceiling_launch_bytes": round(r["achieved"] / rceil_l, 4)}
+                "frac_of_read_ceiling_launch_bytes": round(r["achieved"] / rceil_l, 4),
+                "l2_read_ceiling_by_workgroups": l2c}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
               f"1 GiB streaming read: {rceil:.0f} GB/s, streaming read of one launch's "
-              f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s)", file=sys.stderr, flush=True)
+              f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s; L2-resident read by workgroups: {l2c})",
+              file=sys.stderr, flush=True)
     topk_line = None
     prefill_warm_s = None
     if not args.no_topk_line and not args.top_k and temp > 0:

@@ -640,3 +640,52 @@ extern "C" int32_t fc_read_probe(const void* src, int64_t bytes, uint32_t* out, 
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
+
+// Read of L2-resident data (the ceiling against which the GEMMs' L2-to-CU
+// traffic is rated): workgroup w reads `per_wg` bytes from the region of XCD
+// w % 8 (workgroups are dealt to the eight XCDs round robin, so each XCD's L2
+// holds its own region of `region` bytes), starting at offset 64 KB x (w / 8)
+// and wrapping. Direct global-to-LDS loads (16 bytes per lane), sixteen 1 KB
+// loads in flight per wave, the data landing in a per-wave LDS ring that
+// nothing reads (one word of it is folded into `out` at the end).
+#define L2P_DEPTH 16
+__global__ __launch_bounds__(256) void k_l2_probe(const char* __restrict__ src, int64_t region, int64_t per_wg,
+                                                  uint32_t* __restrict__ out) {
+  __shared__ uint4 ring[4][L2P_DEPTH][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const char* base = src + (int64_t)(blockIdx.x & 7) * region;
+  // each step the workgroup reads 4 KB: wave w the 1 KB at offset 1 KB w
+  int64_t off = ((int64_t)(blockIdx.x >> 3) * 65536) % region;
+  const int64_t steps = per_wg / 4096;
+  for (int64_t it = 0; it < steps; it += L2P_DEPTH) {
+#pragma unroll
+    for (int u = 0; u < L2P_DEPTH; ++u) {
+      __builtin_amdgcn_global_load_lds((const void*)(base + off + wave * 1024 + lane * 16),
+                                       (__attribute__((address_space(3))) void*)&ring[wave][u][0], 16, 0, 0);
+      off += 4096;
+      if (off >= region) off -= region;
+      // at most L2P_DEPTH loads of this wave outstanding
+      __builtin_amdgcn_s_waitcnt(((L2P_DEPTH - 1) & 15) | (((L2P_DEPTH - 1) >> 4) << 14) | (7 << 4) | (15 << 8));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const uint4 v = ring[wave][0][lane];
+  uint32_t x = v.x ^ v.y ^ v.z ^ v.w;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o, WAVE);
+  if (lane == 0) out[blockIdx.x * 4 + wave] = x;
+}
+
+extern "C" int32_t fc_l2_read_probe(const void* src, int64_t region_bytes, int64_t bytes, uint32_t* out,
+                                    int32_t workgroups, void* stream) {
+  FC_CHECK_ARG(src && out, "null pointer");
+  FC_CHECK_ARG(region_bytes >= 65536 && region_bytes % 4096 == 0, "region_bytes: a multiple of 4 KB, >= 64 KB");
+  FC_CHECK_ARG(workgroups > 0 && workgroups <= 65536, "workgroups in [1, 65536]");
+  const int64_t per_wg = bytes / workgroups / (4096 * L2P_DEPTH) * (4096 * L2P_DEPTH);
+  FC_CHECK_ARG(per_wg > 0, "bytes must give each workgroup at least 64 KB");
+  hipLaunchKernelGGL(k_l2_probe, dim3(workgroups), dim3(256), 0, (hipStream_t)stream, (const char*)src,
+                     region_bytes, per_wg, out);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}

@@ -837,6 +837,155 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const bf16_t* __restrict__ A, 
   tile_epilogue<MB, NBW, EPI>(e, acc, rpre, qpre, m0, n0, nt, 0, M, K);
 }
 
+// bf16 MFMA GEMM for verify-size row counts with every operand block in a
+// deep LDS ring fed by direct global-to-LDS loads.
+//
+// A workgroup owns an MT x NT tile (MT = 16 MB rows, NT = 16 NB columns) of
+// one K split; its four waves form a WM x (4 / WM) grid over (row blocks,
+// column blocks). Per 64-wide k chunk the tile needs 2 MB activation and
+// 2 NB weight blocks of 1 KB (fragment order); they go straight into stage
+// chunk % NSTG of the ring, PER per wave, with no registers held by loads in
+// flight. Step i waits until the wave's own loads of chunk i have landed
+// (vmcnt: the NSTG - 2 later chunks may still be in flight), meets the other
+// waves at a barrier (so every wave's part of the stage is visible and every
+// wave has finished reading stage i - 1), refills stage i - 1 with chunk
+// i + NSTG - 1, then reads its fragments of stage i and runs its MFMAs.
+// Each stage is its own LDS object and the loop is unrolled over the ring,
+// so the compiler can tell a stage's reads from the loads into the others.
+// Against the register-staged kernels this keeps NSTG - 1 chunks in flight
+// per workgroup instead of one or two: at the cfg4 verify MLP c_proj shape
+// (224 rows, N 1536, K 6144, 64 x 96 tiles, K split 4: 256 workgroups) it
+// takes 13.4-13.8 us against 15.4 us for the 32 x 64 split-3 tiles of
+// k_gemm_ks (weights cycled from HBM). Measured limits: with the weights
+// resident in L2 its loads alone run at ~120 GB/s per CU (the L2-resident
+// read ceiling), and its LDS traffic (stage writes plus fragment reads,
+// 3x the global bytes at a 2 x 2 wave grid) then bounds it; streaming the
+// weights from HBM adds ~3 us per launch that the ring depth does not hide.
+// Grid: N tile fastest (tile n on XCD n % 8: the M tiles and splits of one
+// weight slab share that XCD's L2), then split, then M tile; tiles past the
+// device row count exit at once.
+template <int TOT>
+struct RingStage {
+  uint4 blk[TOT][64];
+};
+template <int MB, int NB, int NSTG, int WM, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_ring(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
+                                                   int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
+                                                   int S, Epi e) {
+  constexpr int WN = 4 / WM, MBW = MB / WM, NBW = NB / WN;
+  static_assert(MB % WM == 0 && NB % WN == 0, "wave grid");
+  constexpr int TOT = 2 * MB + 2 * NB, PER = (TOT + 3) / 4, NV = PER * (NSTG - 2);
+  static_assert(NV < 64 && NSTG >= 3 && NSTG <= 8, "ring depth / vmcnt range");
+  __shared__ RingStage<TOT> s0, s1, s2, s3, s4, s5, s6, s7;  // the first NSTG are used
+  const int id = blockIdx.x;
+  const int ntiles8 = (ntiles + 7) & ~7;
+  const int nt = id % ntiles8;
+  const int rest = id / ntiles8;
+  const int s = rest % S, mt = rest / S;
+  if (nt >= ntiles) return;
+  const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
+  const int m0 = mt * 16 * MB;
+  if (m0 >= M) return;
+  const int n0 = nt * 16 * NB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int r = lane & 15, g = lane >> 4;
+  const int C = K >> 6;
+  const int c_beg = (int)((int64_t)s * C / S), c_end = (int)((int64_t)(s + 1) * C / S);
+  const int n = c_end - c_beg;
+  const int64_t KS32 = K >> 5;
+  const int last_blk = (M - 1) >> 4;
+  // this wave's blocks of a chunk: q < 2 MB activation row block q / 2, else
+  // weight column block (q - 2 MB) / 2; k step q % 2. A wave with fewer than
+  // PER distinct blocks repeats the last one (the same bytes into the same
+  // LDS slot, harmless).
+  const bf16_t* src[PER];
+  int dst[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int q = min(wave + 4 * u, TOT - 1);
+    dst[u] = q;
+    if (q < 2 * MB) {
+      src[u] = A + ((int64_t)min(m0 / 16 + (q >> 1), last_blk) * KS32 + (q & 1)) * 512 + lane * 8;
+    } else {
+      const int j2 = q - 2 * MB;
+      src[u] = W + ((int64_t)(n0 / 16 + (j2 >> 1)) * KS32 + (j2 & 1)) * 512 + lane * 8;
+    }
+  }
+  f32x4 acc[MBW][NBW];
+#pragma unroll
+  for (int i = 0; i < MBW; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#define RING_STG(k) (k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : k == 3 ? s3 : k == 4 ? s4 : k == 5 ? s5 : k == 6 ? s6 : s7)
+#define RING_ISSUE(k, c_)                                                                                  \
+  {                                                                                                        \
+    const int64_t cc_ = (int64_t)(c_beg + min((c_), n - 1)) * 1024; /* past the end: harmless re-reads */  \
+    _Pragma("unroll") for (int u = 0; u < PER; ++u)                                                        \
+      __builtin_amdgcn_global_load_lds((const void*)(src[u] + cc_),                                        \
+                                       (__attribute__((address_space(3))) void*)&RING_STG(k).blk[dst[u]][0], \
+                                       16, 0, 0);                                                          \
+  }
+#define RING_STEP(k, i_)                                                                                   \
+  {                                                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                                     \
+    __builtin_amdgcn_s_waitcnt((NV & 15) | ((NV >> 4) << 14) | (7 << 4) | (15 << 8));                      \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                                     \
+    __builtin_amdgcn_s_barrier();                                                                          \
+    __builtin_amdgcn_sched_barrier(0);                                                                     \
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                               \
+    RING_ISSUE(((k) + NSTG - 1) % NSTG, (i_) + NSTG - 1);                                                  \
+    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                                     \
+      v4u af[MBW], wf[NBW];                                                                                \
+      _Pragma("unroll") for (int i = 0; i < MBW; ++i)                                                      \
+        af[i] = __builtin_bit_cast(v4u, RING_STG(k).blk[2 * (wm * MBW + i) + ks][lane]);                   \
+      _Pragma("unroll") for (int j = 0; j < NBW; ++j)                                                      \
+        wf[j] = __builtin_bit_cast(v4u, RING_STG(k).blk[2 * MB + 2 * (wn * NBW + j) + ks][lane]);          \
+      _Pragma("unroll") for (int i = 0; i < MBW; ++i)                                                      \
+        _Pragma("unroll") for (int j = 0; j < NBW; ++j) acc[i][j] = mfma16(af[i], wf[j], acc[i][j]);       \
+    }                                                                                                      \
+  }
+  if (n > 0) {
+#pragma unroll
+    for (int c = 0; c < NSTG - 1; ++c) RING_ISSUE(c, c);
+    int i = 0;
+    for (; i + NSTG <= n; i += NSTG) {
+      RING_STEP(0, i);
+      RING_STEP(1, i + 1);
+      RING_STEP(2, i + 2);
+      if (NSTG > 3) RING_STEP(3 % NSTG, i + 3);
+      if (NSTG > 4) RING_STEP(4 % NSTG, i + 4);
+      if (NSTG > 5) RING_STEP(5 % NSTG, i + 5);
+      if (NSTG > 6) RING_STEP(6 % NSTG, i + 6);
+      if (NSTG > 7) RING_STEP(7 % NSTG, i + 7);
+    }
+    // the last n - i < NSTG chunks sit in stages 0 .. n - i - 1
+    if (i < n) RING_STEP(0, i);
+    if (i + 1 < n) RING_STEP(1, i + 1);
+    if (NSTG > 3 && i + 2 < n) RING_STEP(2, i + 2);
+    if (NSTG > 4 && i + 3 < n) RING_STEP(3 % NSTG, i + 3);
+    if (NSTG > 5 && i + 4 < n) RING_STEP(4 % NSTG, i + 4);
+    if (NSTG > 6 && i + 5 < n) RING_STEP(5 % NSTG, i + 5);
+    if (NSTG > 7 && i + 6 < n) RING_STEP(6 % NSTG, i + 6);
+  }
+#undef RING_STEP
+#undef RING_ISSUE
+#undef RING_STG
+  __builtin_amdgcn_s_waitcnt(0);  // no direct load outlives the workgroup's LDS
+  Epi ee = e;
+  ee.split = s;
+#pragma unroll
+  for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * (wm * MBW + mb) + 4 * g + i;
+        if (m < M) epi_apply<EPI, true>(ee, m, n0 + 16 * (wn * NBW + j) + r, acc[mb][j][i]);
+      }
+}
+
 // bf16 MFMA GEMM for prefill-size row counts (M >= FC_BIG_M, N % 256 == 0,
 // K % 128 == 0).
 //
@@ -1192,6 +1341,16 @@ static void launch_dma(const void* A, const void* W, int Mcap, const int* Mdev, 
                                            (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, mtiles, mfast, e));
 }
 
+// the verify MLP c_proj's ring tile: 64 x 96, 5 stages, 2 x 2 waves
+template <int MB, int NB, int NSTG, int WM>
+static void launch_ring(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int S, const Epi& e,
+                        hipStream_t s) {
+  const int ntiles = N / (16 * NB), mtiles = (Mcap + 16 * MB - 1) / (16 * MB);
+  const int nwg = (ntiles + 7) / 8 * 8 * S * mtiles;
+  FC_EPI_SWITCH(e.mode, hipLaunchKernelGGL((k_gemm_ring<MB, NB, NSTG, WM, E>), dim3(nwg), dim3(256), 0, s,
+                                           (const bf16_t*)A, (const bf16_t*)W, Mcap, Mdev, N, K, ntiles, S, e));
+}
+
 template <int EPI, int NB>
 static void launch_big_e(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
                          hipStream_t s) {
@@ -1236,10 +1395,14 @@ static void launch_la_qkv(const void* A, const void* W, int Mcap, const int* Mde
 // Mcap rows; tiles past the device-side count exit at once).
 struct GemmPlan {
   bool gemv, la, dma, big;  // VALU GEMV (fp32) / LDS-shared-A / LDS-ring / 256 x 256 (else the K-split kernel)
+  bool ring;                // deep direct-load ring, 64 x 96 tiles (k_gemm_ring)
   int mb, nb, S;       // k_gemm_ks: 16 mb x 16 nb tile; k_gemm_la, k_gemm_dma: 16 mb x 64 nb tile
 };
 #ifndef FC_GEMM_DMA
 #define FC_GEMM_DMA 1
+#endif
+#ifndef FC_GEMM_RING
+#define FC_GEMM_RING 1
 #endif
 // Row counts from which the layer GEMMs below the 256 x 256 kernel take the
 // larger tiles (large-batch verify chunks, e.g. 128 rows x 9 tokens): c_fc
@@ -1297,6 +1460,16 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
       p.dma = true;
       p.mb = 4;
       p.nb = 1;
+      return p;
+    }
+    // verify chunks below FC_MID_M rows whose residual GEMM has n_embd = a
+    // multiple of 96 columns: the deep-ring 64 x 96 tiles with a 4-way split
+    // (cfg4's MLP c_proj: 16 x 4 tiles x 4 splits = 256 workgroups)
+    if (FC_GEMM_RING && Mtyp > 160 && N % 96 == 0 && C % 4 == 0 && s_max >= 4) {
+      p.ring = true;
+      p.mb = 4;
+      p.nb = 6;
+      p.S = 4;
       return p;
     }
     // 33-160 rows (large-batch draft steps): 32 x 32 tiles, 4-way split;
@@ -1409,6 +1582,9 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
     FC_CHECK_ARG(ee.mode != EPI_PARTIAL && ee.rms_in == nullptr && ee.xa == nullptr,
                  "the 256 x 256 GEMM has no split-K or folded-norm epilogue");
     launch_big(A, W, Mcap, Mdev, N, K, ee, s);
+  } else if (p.ring) {
+    FC_CHECK_ARG(ee.rms_in == nullptr && ee.xa == nullptr, "the ring GEMM has no folded-norm epilogue");
+    launch_ring<4, 6, 5, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);
   } else if (p.dma) {
     launch_dma<4, 1>(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.la) {

@@ -324,6 +324,17 @@ int32_t fc_cross_entropy(const float* logits, int64_t row_stride, const int32_t*
  * are rated next to the 8 TB/s peak. */
 int32_t fc_read_probe(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups, void* stream);
 
+/* Read of L2-resident data: workgroup w (256 threads) reads
+ * bytes / workgroups bytes (rounded down to 64 KB) from the region of
+ * `region_bytes` at src + (w % 8) * region_bytes (workgroups go to the
+ * eight XCDs round robin, so each XCD's L2 holds one region; src must hold
+ * 8 * region_bytes), wrapping, with direct global-to-LDS loads, sixteen 1 KB
+ * loads in flight per wave; out receives 4 * workgroups words. No
+ * counterpart in the reference: the ceiling against which the GEMMs'
+ * L2-to-CU traffic is rated (MI355X: 4 MB of L2 per XCD). */
+int32_t fc_l2_read_probe(const void* src, int64_t region_bytes, int64_t bytes, uint32_t* out, int32_t workgroups,
+                         void* stream);
+
 /* Stream capture into a replayable hipGraph (the captured draft loop). */
 int32_t fc_graph_begin(void* stream);
 int32_t fc_graph_end(void* stream, void** exec_out);
