@@ -1059,6 +1059,13 @@ __global__ __launch_bounds__(256) void k_gemm_ring(const bf16_t* __restrict__ A,
 #ifndef FC_BIG_MIN_TILES
 #define FC_BIG_MIN_TILES 224
 #endif
+// Wide outputs (the lm_head, N >= 16384) take the 256 x 256 tiles from this
+// many rows: the cfg4 verify head (224 rows, 256 tiles) runs 78.7 us on them
+// against 92.7 us on the LDS-shared 128 x 128 tiles (kernel trace); the
+// round gains ~3 us of it (4.814-4.818 vs 4.817-4.820 ms, alternating builds).
+#ifndef FC_BIG_HEAD_M
+#define FC_BIG_HEAD_M 200
+#endif
 template <int NB>
 struct BigStage {
   uint4 a[16][64];
@@ -1472,7 +1479,7 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     p.gemv = true;
     return p;
   }
-  if (Mtyp >= FC_BIG_M && N % 256 == 0 && K % 128 == 0) {
+  if (Mtyp >= (N >= 16384 ? FC_BIG_HEAD_M : FC_BIG_M) && N % 256 == 0 && K % 128 == 0) {
     // prefill chunks: 256 x 256 (or 256 x 192) tiles, MFMA-bound, when there
     // are enough of them to occupy the CUs (verify-size M of ~1200 rows gives
     // 5 M tiles: the 64-row kernels are faster there)
@@ -1571,8 +1578,18 @@ static GemmPlan plan_relu2(int Mtyp, int N, int K, int dtype) {
   return p;
 }
 
+// Up to this many typical rows (one-row decode: cfg2's 5-token verify and
+// 1-token draft steps) the QKV GEMM takes one-head 32 x 128 tiles and
+// finishes the attention prologue itself, saving the k_prologue dispatch:
+// cfg2 0.923-0.927 vs 0.952-0.956 ms per round (alternating builds). At 32
+// rows (cfg4's draft steps: 36 workgroups over 14 MB) the separate
+// prologue is faster.
+#ifndef FC_QKV_TINY_M
+#define FC_QKV_TINY_M 16
+#endif
 bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim) {
   if (dtype != FC_BF16 || head_dim != 128 || N % 128 != 0 || K % 64 != 0) return false;
+  if (Mtyp <= FC_QKV_TINY_M) return true;
   const GemmPlan p = plan_gemm(Mtyp, N, K, dtype, false);
   // the QKV tile itself is k_gemm_la's 32 x 128 (64 x 128 from FC_MID_M rows), or a 128 x 128 quadrant of k_gemm_big
   return p.big || p.dma || (p.la && p.mb == 2 && p.nb == 2);

@@ -547,10 +547,11 @@ def test_attn_prologue_vs_oracle(dtype):
 
 
 # ---------------------------------------------------------------- fused QKV epilogue
-@pytest.mark.parametrize("dtype,M", [("fp32", 40), ("bf16", 40), ("bf16", 13)])
+@pytest.mark.parametrize("dtype,M", [("fp32", 40), ("bf16", 40), ("bf16", 24)])
 def test_attn_qkv_unfused_fallback(dtype, M):
-    """fc_attn_qkv below the fused-epilogue row counts (bf16 with 13 or 40
-    tokens) and for fp32 models takes the unfused path: the QKV GEMM into
+    """fc_attn_qkv between the fused-epilogue row counts (bf16 with 24 or 40
+    tokens: above the one-row decode sizes, below the verify sizes) and for
+    fp32 models takes the unfused path: the QKV GEMM into
     the caller's workspace, then the prologue kernel. Its q, K and V must
     equal fc_gemm followed by fc_attn_prologue on the same inputs exactly
     (the same kernels with the same plan), GQA 12 / 4 with a value-embedding
@@ -602,12 +603,14 @@ def test_attn_qkv_unfused_fallback(dtype, M):
         assert qa[3].float().abs().sum().item() == 0, "the skipped token wrote q"
 
 
-@pytest.mark.parametrize("H,G,M", [(12, 4, 130), (12, 12, 224), (12, 4, 1000), (12, 12, 3400)])
+@pytest.mark.parametrize("H,G,M", [(12, 4, 6), (12, 12, 16), (12, 4, 130), (12, 12, 224), (12, 4, 1000),
+                                   (12, 12, 3400)])
 def test_attn_qkv_fused_vs_prologue(H, G, M):
-    """fc_attn_qkv at verify / prefill row counts runs the attention
-    prologue inside the QKV GEMM's epilogue (the 32 x 128 tile of the
-    LDS-shared kernel; its 64 x 128 tile, two 32-token passes, from 832
-    rows; at 3400 rows the 256 x 256 tile's quadrants). Its q
+    """fc_attn_qkv at one-row decode sizes (up to 16 tokens), verify and
+    prefill row counts runs the attention prologue inside the QKV GEMM's
+    epilogue (the 32 x 128 tile of the LDS-shared kernel; its 64 x 128
+    tile, two 32-token passes, from 832 rows; at 3400 rows the 256 x 256
+    tile's quadrants). Its q
     and the K / V it appends (RoPE, 1.2 * RMSNorm, the value-embedding gate
     on the V heads) must equal fc_gemm's fp32 projection of the same input
     followed by fc_attn_prologue, element by element within 1e-2 relative
