@@ -172,6 +172,34 @@ def read_ceiling(dev, n_bytes=1 << 30, n_rep=5, n_buf=1, grids=(1024, 2048, 4096
     return best
 
 
+def walk_ceiling(dev, units, n_bytes, n_rep=5, n_buf=3):
+    """The verify attention's own load walk without its compute
+    (fc_walk_probe): `units` workgroups (rows x KV groups), each reading its
+    share of `n_bytes` as 16 KB tiles, four waves taking every fourth tile
+    with sixteen 1 KB non-temporal loads each; `n_buf` buffers read in turn
+    so no launch finds its bytes in the Infinity Cache. GB/s."""
+    import torch
+    from flaxchat_amd import _lib
+    tiles = max(1, int(round(n_bytes / (units * 16384))))
+    nb = units * tiles * 16384
+    srcs = [torch.ones(nb, dtype=torch.uint8, device=dev) for _ in range(n_buf)]
+    out = torch.empty(256 * units, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev)
+    run = lambda i: _lib.check(_lib.lib().fc_walk_probe(srcs[i % n_buf].data_ptr(), units, tiles,  # noqa: E731
+                                                        out.data_ptr(), s.cuda_stream), "fc_walk_probe")
+    for i in range(n_buf):
+        run(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(n_rep * n_buf):
+        run(i)
+    e1.record(s)
+    e1.synchronize()
+    res = nb * n_rep * n_buf / (e0.elapsed_time(e1) / 1e3) / 1e9
+    del srcs, out
+    return res
+
+
 def l2_ceiling(dev, region=1 << 20, n_bytes=1 << 30, n_rep=5, grids=(256, 512, 1024)):
     """Measured L2-to-CU read ceiling: fc_l2_read_probe (each XCD's workgroups
     read a 1 MB region that stays in that XCD's L2, direct-to-LDS loads)
@@ -392,6 +420,8 @@ def main():
         rceil_l = read_ceiling(target.device, n_bytes=int(r["per_launch_bytes"]), n_buf=3,
                                grids=(256, 512, 1024, 2048, 4096))
         l2c = l2_ceiling(target.device)
+        # the attention's own grid and tile walk without its compute
+        wceil = walk_ceiling(target.device, sess.B * sess.T.G, int(r["per_launch_bytes"]))
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
@@ -402,10 +432,12 @@ def main():
                 "read_ceiling": round(rceil, 1), "frac_of_read_ceiling": round(r["achieved"] / rceil, 4),
                 "read_ceiling_launch_bytes": round(rceil_l, 1),
                 "frac_of_read_ceiling_launch_bytes": round(r["achieved"] / rceil_l, 4),
+                "walk_ceiling": round(wceil, 1), "frac_of_walk_ceiling": round(r["achieved"] / wceil, 4),
                 "l2_read_ceiling_by_workgroups": l2c}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
               f"1 GiB streaming read: {rceil:.0f} GB/s, streaming read of one launch's "
-              f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s; L2-resident read by workgroups: {l2c})",
+              f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s; its own load walk: {wceil:.0f} GB/s; "
+              f"L2-resident read by workgroups: {l2c})",
               file=sys.stderr, flush=True)
     topk_line = None
     prefill_warm_s = None

@@ -689,3 +689,33 @@ extern "C" int32_t fc_l2_read_probe(const void* src, int64_t region_bytes, int64
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
+
+// The decode attention's load pattern with no compute: workgroup u (4
+// waves) walks unit u's `tiles` contiguous 16 KB tiles (a 32-key K block and
+// its V block), wave w taking tiles w, w + 4, ...; per tile each wave issues
+// sixteen 1 KB non-temporal loads (16 bytes per lane) and waits for them,
+// as k_attn_mfma does. The rate the attention can reach with its grid and
+// tile walk, whatever its MFMA and softmax work.
+__global__ __launch_bounds__(256) void k_walk_probe(const rp_u32x4* __restrict__ src, int tiles,
+                                                    uint32_t* __restrict__ out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const char* ub = (const char*)src + (int64_t)blockIdx.x * tiles * 16384;
+  rp_u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int t = wave; t < tiles; t += 4) {
+    const rp_u32x4* p = (const rp_u32x4*)(ub + (int64_t)t * 16384) + lane;
+    rp_u32x4 r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = __builtin_nontemporal_load(p + 64 * i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc ^= r[i];
+  }
+  out[blockIdx.x * 256 + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+extern "C" int32_t fc_walk_probe(const void* src, int32_t units, int32_t tiles, uint32_t* out, void* stream) {
+  FC_CHECK_ARG(src && out, "null pointer");
+  FC_CHECK_ARG(units > 0 && units <= 65535 && tiles > 0, "units in [1, 65535], tiles > 0");
+  hipLaunchKernelGGL(k_walk_probe, dim3(units), dim3(256), 0, (hipStream_t)stream, (const rp_u32x4*)src, tiles, out);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}

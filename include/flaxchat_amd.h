@@ -335,6 +335,15 @@ int32_t fc_read_probe(const void* src, int64_t bytes, uint32_t* out, int32_t wor
 int32_t fc_l2_read_probe(const void* src, int64_t region_bytes, int64_t bytes, uint32_t* out, int32_t workgroups,
                          void* stream);
 
+/* The decode attention's load pattern without its compute: workgroup u of
+ * `units` reads the `tiles` consecutive 16 KB tiles at src + u * tiles *
+ * 16384 (src must hold units * tiles * 16384 bytes), each of its four waves
+ * taking every fourth tile as sixteen 1 KB non-temporal loads, as
+ * k_attn_mfma walks a (row, KV group)'s K and V blocks; out receives
+ * 256 * units words. No counterpart in the reference: the rate the verify
+ * attention can reach with its grid and tile walk. */
+int32_t fc_walk_probe(const void* src, int32_t units, int32_t tiles, uint32_t* out, void* stream);
+
 /* Stream capture into a replayable hipGraph (the captured draft loop). */
 int32_t fc_graph_begin(void* stream);
 int32_t fc_graph_end(void* stream, void** exec_out);

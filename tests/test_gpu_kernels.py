@@ -663,3 +663,29 @@ def test_attn_qkv_fused_vs_prologue(H, G, M):
             assert scale > 0 and rel <= 1e-2, f"layer {layer} {name}"
         # the skipped token (row -1) wrote no q either
         assert qa[3].abs().sum().item() == 0 and qb[3].abs().sum().item() == 0
+
+
+# ---------------------------------------------------------------- measurement probes
+def test_walk_probe_reads_each_units_tiles():
+    """fc_walk_probe (the attention's load walk, timed by bench.py): every
+    thread's output word is the XOR of the 16-byte groups it loaded, so a
+    host recomputation over the expected addresses (unit u's tiles at
+    u * tiles * 16 KB, wave w taking tiles w, w + 4, ..., lane l the groups
+    l + 64 i of a tile) checks that it reads exactly its units' bytes."""
+    units, tiles = 5, 6
+    rng = np.random.default_rng(31)
+    words = rng.integers(0, 2**32, units * tiles * 4096, dtype=np.uint64).astype(np.uint32)
+    src = torch.from_numpy(words.view(np.int32)).to(dev())
+    out = torch.zeros(256 * units, dtype=torch.int32, device=dev())
+    check(_lib.lib().fc_walk_probe(src.data_ptr(), units, tiles, out.data_ptr(), stream()), "fc_walk_probe")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32).reshape(units, 4, 64)
+    g16 = words.reshape(units, tiles, 1024, 4)  # 16-byte groups of each tile
+    want = np.zeros((units, 4, 64), np.uint32)
+    for w in range(4):
+        for t in range(w, tiles, 4):
+            for i in range(16):
+                grp = g16[:, t, np.arange(64) + 64 * i, :]  # [units, lane, 4 words]
+                want[:, w, :] ^= np.bitwise_xor.reduce(grp, axis=-1)
+    assert np.array_equal(got, want)
+    assert _lib.lib().fc_walk_probe(src.data_ptr(), 0, tiles, out.data_ptr(), stream()) != 0  # refused
