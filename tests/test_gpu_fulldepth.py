@@ -192,3 +192,52 @@ def test_fulldepth_bf16_vs_oracle(name):
     assert v[0] <= BOUNDS["verify"][0] and v[1] <= BOUNDS["verify"][1], f"verify chunk {v}"
     assert d[0] <= BOUNDS["draft"][0] and d[1] <= BOUNDS["draft"][1], f"draft step {d}"
     assert g <= BOUNDS["generate"][1] and frac >= 0.95, f"generate: gap {g}, argmax fraction {frac}"
+
+
+def test_verify_chunk_rows_past_one_query_block():
+    """A verify-size chunk whose typical row fills one 16-column query block
+    (7 tokens) while some rows feed 20 (a long rollback's backlog), so the
+    decode attention's second query block holds queries for those rows
+    only. Logits of the live tokens of long and short rows against the fp32
+    oracle (2 layers at the cfg4 width, bf16-rounded weights)."""
+    from flaxchat_amd.gpt import GPT
+    cfg = GPTConfig(sequence_len=1024, vocab_size=8192, n_layer=2, n_head=12, n_kv_head=12, n_embd=1536,
+                    window_pattern="SL", short_window=64)
+    host = GPT.init_normal_parallel(cfg, seed=12)
+    host.wte.embedding = _round_bf16(host.wte.embedding)
+    host.lm_head.kernel = _round_bf16(host.lm_head.kernel)
+    for blk in host.blocks:
+        for lin in (blk.attn.c_q, blk.attn.c_k, blk.attn.c_v, blk.attn.c_proj, blk.mlp.c_fc, blk.mlp.c_proj):
+            lin.kernel = _round_bf16(lin.kernel)
+    for ve in host.value_embeds.values():
+        ve.embedding = _round_bf16(ve.embedding)
+    dm = DeviceModel.from_host(host, dtype="bf16")
+    rng = np.random.default_rng(13)
+    B, n_out = 32, 20
+    lens = {b: int(rng.integers(1, 200)) for b in range(B)}
+    n_new = {b: (20 if b in (3, 17, 30) else 7) for b in range(B)}
+    rows = {b: rng.integers(0, 8192, n).tolist() for b, n in lens.items()}
+    new = {b: rng.integers(0, 8192, n_new[b]).tolist() for b in range(B)}
+    _say("verify chunk: 32 rows, 3 of them with 20 tokens, typical 7 per row")
+    dev = dm.device
+    cache = DeviceCache(dm, B, 512)
+    ws = Workspace(dev)
+    prefill_rows(dm, cache, [rows[b] for b in range(B)], [0] * B, ws)
+    tok, off, _ = pack_rows([new[b] for b in range(B)])
+    max_tokens = 704
+    tokens = torch.zeros(max_tokens, dtype=torch.int32, device=dev)
+    tokens[:len(tok)] = torch.from_numpy(tok).to(dev)
+    starts = np.asarray([lens[b] for b in range(B)], np.int32)
+    logits = torch.zeros(B, n_out, dm.V, dtype=torch.float32, device=dev)
+    forward_packed(dm, cache, tokens, torch.from_numpy(off).to(dev), torch.from_numpy(starts).to(dev), 22, n_out,
+                   logits, ws, typ_tokens=B * 7)
+    torch.cuda.synchronize()
+    lg = logits.cpu().numpy()
+    worst = 0.0
+    for b in (0, 3, 17, 21, 30):
+        k = n_new[b]
+        ref = _oracle_logits(host, rows[b] + new[b])[-k:]
+        e, g = _compare(f"row {b} ({k} tokens)", lg[b, n_out - k:], ref)
+        worst = max(worst, e)
+        assert g <= 4e-2, f"row {b}: argmax gap {g}"
+    assert worst <= 2e-2
