@@ -14,11 +14,15 @@
 //              steps and the split-K residual GEMMs.
 //   k_gemm_la  bf16 MFMA, 32-128 rows x 128 columns, the four waves split
 //              the columns and share the activation tile through LDS;
-//              verify row counts and the verify lm_head.
+//              verify row counts, the QKV GEMM with its fused attention
+//              prologue (also at one-row decode sizes) and the draft lm_head.
 //   k_gemm_dma bf16 MFMA, 64 x 64 tiles fed by direct global-to-LDS loads
 //              into a 4-stage ring; verify c_fc.
+//   k_gemm_ring bf16 MFMA, 64 x 96 tiles, a 5-stage direct-load LDS ring;
+//              the verify MLP c_proj (K split 4).
 //   k_gemm_big bf16 MFMA, 256 x 256 tiles, 4-stage LDS ring of direct
-//              loads; prefill chunks (M >= 1024).
+//              loads; prefill chunks (M >= 1024) and the lm_head from 200
+//              rows (the verify head).
 // The row count may be a device value (packed token chunks whose size is
 // only known on the GPU): the grid covers the capacity and tiles past the
 // actual count exit at once.
