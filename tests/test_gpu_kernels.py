@@ -689,3 +689,31 @@ def test_walk_probe_reads_each_units_tiles():
                 want[:, w, :] ^= np.bitwise_xor.reduce(grp, axis=-1)
     assert np.array_equal(got, want)
     assert _lib.lib().fc_walk_probe(src.data_ptr(), 0, tiles, out.data_ptr(), stream()) != 0  # refused
+
+
+def test_l2_read_probe_reads_its_region():
+    """fc_l2_read_probe (the L2-to-CU ceiling bench.py reports): workgroup w
+    walks 4 KB steps through the region of XCD w % 8 from offset
+    (w / 8) * 64 KB, wave v loading the 1 KB at 1 KB v of each step into LDS
+    slot (step % 16); its output word is the XOR over lanes of slot 0, the
+    last step whose index is a multiple of 16. A host recomputation of those
+    addresses checks the walk stays in its region."""
+    region, wgs, per_wg = 64 << 10, 16, 256 << 10  # 64 steps per workgroup
+    rng = np.random.default_rng(41)
+    words = rng.integers(0, 2**32, 8 * region // 4, dtype=np.uint64).astype(np.uint32)
+    src = torch.from_numpy(words.view(np.int32)).to(dev())
+    out = torch.zeros(4 * wgs, dtype=torch.int32, device=dev())
+    check(_lib.lib().fc_l2_read_probe(src.data_ptr(), region, per_wg * wgs, out.data_ptr(), wgs, stream()),
+          "fc_l2_read_probe")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32).reshape(wgs, 4)
+    steps = per_wg // 4096
+    want = np.zeros((wgs, 4), np.uint32)
+    for w in range(wgs):
+        off = ((w // 8) * 65536 + 4096 * 16 * ((steps - 1) // 16)) % region
+        base = (w % 8) * region + off
+        for v in range(4):
+            blk = words[(base + 1024 * v) // 4:(base + 1024 * v + 1024) // 4]
+            want[w, v] = np.bitwise_xor.reduce(blk)
+    assert np.array_equal(got, want)
+    assert _lib.lib().fc_l2_read_probe(src.data_ptr(), 1000, per_wg * wgs, out.data_ptr(), wgs, stream()) != 0
