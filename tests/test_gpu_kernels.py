@@ -717,3 +717,27 @@ def test_l2_read_probe_reads_its_region():
             want[w, v] = np.bitwise_xor.reduce(blk)
     assert np.array_equal(got, want)
     assert _lib.lib().fc_l2_read_probe(src.data_ptr(), 1000, per_wg * wgs, out.data_ptr(), wgs, stream()) != 0
+
+
+def test_read_probe_reads_each_share():
+    """fc_read_probe (the HBM read ceiling bench.py reports): workgroup b
+    streams the 16-byte entries [b per, (b + 1) per) of the buffer, thread
+    t the entries t, t + 256, ...; wave v's output word is the XOR of its
+    threads' entries, recomputed here (including a ragged last share)."""
+    n16, wgs = 10000, 7
+    rng = np.random.default_rng(43)
+    words = rng.integers(0, 2**32, n16 * 4, dtype=np.uint64).astype(np.uint32)
+    src = torch.from_numpy(words.view(np.int32)).to(dev())
+    out = torch.zeros(4 * wgs, dtype=torch.int32, device=dev())
+    check(_lib.lib().fc_read_probe(src.data_ptr(), n16 * 16, out.data_ptr(), wgs, stream()), "fc_read_probe")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32).reshape(wgs, 4)
+    e = np.bitwise_xor.reduce(words.reshape(n16, 4), axis=1)  # each entry's 4 words
+    per = (n16 + wgs - 1) // wgs
+    want = np.zeros((wgs, 4), np.uint32)
+    for b in range(wgs):
+        j = np.arange(b * per, min((b + 1) * per, n16))
+        wave = ((j - b * per) % 256) // 64
+        for v in range(4):
+            want[b, v] = np.bitwise_xor.reduce(e[j[wave == v]]) if (wave == v).any() else 0
+    assert np.array_equal(got, want)
