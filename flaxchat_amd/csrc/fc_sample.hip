@@ -787,8 +787,9 @@ __device__ __forceinline__ TkRow tk_finish_row(const TkChunk* __restrict__ ch, i
 #pragma unroll
     for (int q = 0; q < TK_SPT; ++q)
       if (ok[q]) {
-        const float p = in[q] ? expf(zv[q] / T - mx) / sum : 0.f;
-        argmax_merge(bv, bi, logf(fmaxf(p, 1e-10f)) + gv[q], iv[q]);
+        // outside the keep set p = 0, whose log(max(p, 1e-10)) is lfl
+        const float lp = in[q] ? logf(fmaxf(expf(zv[q] / T - mx) / sum, 1e-10f)) : lfl;
+        argmax_merge(bv, bi, lp + gv[q], iv[q]);
       }
     for (int cc = threadIdx.x; cc < nch; cc += TK_THR) argmax_merge(bv, bi, lfl + ch[cc].g, ch[cc].gi);
     block_argmax(bv, bi, redv, redi);
