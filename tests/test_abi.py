@@ -52,6 +52,16 @@ def test_argument_errors_are_status_codes():
     assert L.fc_attn_prologue(ctypes.byref(m), 0, ctypes.byref(c), None, None, None, None, None, 1, None, None) == -1
     assert b"null" in L.fc_last_error()
     assert L.fc_attn_qkv(ctypes.byref(m), 0, ctypes.byref(c), None, None, None, None, 1, 0, None, None, 0, None) == -1
+    # the measurement probes refuse null pointers and bad sizes before any GPU call
+    p = ctypes.c_void_p(0x1000)
+    assert L.fc_read_probe(None, 4096, p, 1, None) == -1 and b"null" in L.fc_last_error()
+    assert L.fc_read_probe(p, 4100, p, 1, None) == -1
+    assert L.fc_read_probe(p, 4096, p, 0, None) == -1
+    assert L.fc_l2_read_probe(p, 1000, 1 << 20, p, 8, None) == -1
+    assert L.fc_l2_read_probe(p, 65536, 1 << 10, p, 8, None) == -1  # under 64 KB per workgroup
+    assert L.fc_walk_probe(None, 4, 2, p, None) == -1 and b"null" in L.fc_last_error()
+    assert L.fc_walk_probe(p, 0, 2, p, None) == -1
+    assert L.fc_walk_probe(p, 4, 0, p, None) == -1
 
 
 def test_noalloc_refuses_sizes_beyond_scratch():
