@@ -1076,7 +1076,8 @@ struct BigStage {
   uint4 w[4 * NB][64];
 };
 template <int EPI>
-__device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0, float v1, float v2, float v3) {
+__device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0, float v1, float v2, float v3,
+                                           int split) {
   if constexpr (EPI == EPI_STORE) {
     *(float4*)((float*)e.out + (int64_t)m * e.ldo + n) = float4{v0, v1, v2, v3};
   } else if constexpr (EPI == EPI_ADD) {
@@ -1101,6 +1102,8 @@ __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0,
       const float4 x0 = *(const float4*)(e.x0 + i);
       *xp = float4{e.r * t.x + e.a * x0.x, e.r * t.y + e.a * x0.y, e.r * t.z + e.a * x0.z, e.r * t.w + e.a * x0.w};
     }
+  } else if constexpr (EPI == EPI_PARTIAL) {  // split-K partial, finished by the next RMSNorm
+    *(float4*)(e.part + ((int64_t)split * e.part_rows + m) * e.ldo + n) = float4{v0, v1, v2, v3};
   } else if constexpr (EPI == EPI_SOFTCAP) {  // logits row (m / n_out, m % n_out), columns past V dropped
     const int b = m / e.n_out, rr = m - b * e.n_out;
     float* o = (float*)e.out + (int64_t)b * e.row_stride + (int64_t)rr * e.V + n;
@@ -1124,18 +1127,33 @@ __device__ __forceinline__ void big_store4(const Epi& e, int m, int n, float v0,
 template <int EPI, int NB>
 __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W,
                                                   int Mcap, const int* __restrict__ Mdev, int N, int K, int ntiles,
-                                                  int mtiles, int per_xcd, Epi e) {
+                                                  int mtiles, int per_xcd, int S, Epi e) {
   // NB 32-column blocks per wave: tile 256 x 64 NB (NB = 4: 256 x 256; NB = 3: 256 x 192)
   constexpr int NSTG = 4, GM = 4, NT = 64 * NB;
   static_assert(NB == 3 || NB == 4, "tile widths 192 and 256");
   static_assert(EPI != EPI_QKV || NB == 4, "the QKV epilogue needs one head (128 columns) per wave");
   __shared__ BigStage<NB> s0, s1, s2, s3;
-  // tile of this workgroup: XCD id % 8 takes grouped tiles [x per_xcd, (x + 1) per_xcd)
-  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if ((int)(blockIdx.x >> 3) >= per_xcd || t >= ntiles * mtiles) return;
-  const int grp = t / (GM * ntiles), rr = t - grp * GM * ntiles;
-  const int gm = min(GM, mtiles - grp * GM);
-  const int nt = rr / gm, mt = grp * GM + rr % gm;
+  // tile of this workgroup. Unsplit: XCD id % 8 takes grouped tiles
+  // [x per_xcd, (x + 1) per_xcd). Split 8 ways in K (EPI_PARTIAL): XCD x
+  // takes split x, whose workgroups share its A and W slabs in that XCD's L2,
+  // M tile slowest, so the live tiles (below the device row count) come
+  // first and the plan keeps them within the XCD's 32 CUs.
+  int sp, nt, mt;
+  if (S == 8) {
+    sp = blockIdx.x & 7;
+    const int j = blockIdx.x >> 3;
+    if (j >= ntiles * mtiles) return;
+    mt = j / ntiles;
+    nt = j - mt * ntiles;
+  } else {
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if ((int)(blockIdx.x >> 3) >= per_xcd || t >= ntiles * mtiles) return;
+    const int grp = t / (GM * ntiles), rr = t - grp * GM * ntiles;
+    const int gm = min(GM, mtiles - grp * GM);
+    nt = rr / gm;
+    mt = grp * GM + rr % gm;
+    sp = 0;
+  }
   const int M = Mdev ? min(*Mdev, Mcap) : Mcap;
   const int m0 = mt * 256;
   if (m0 >= M) return;
@@ -1143,15 +1161,17 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t KS32 = K >> 5;
-  const int C = K >> 5;
+  // this split's 32-deep k steps [c0, c0 + C); the host makes C a multiple of 4
+  const int c0 = (int)(sp * KS32 / S), C = (int)((sp + 1) * KS32 / S) - c0;
   const int last_blk = (M - 1) >> 4;
   // this wave's loads: activation row blocks 4 wave .. +3 and weight column blocks NB wave .. +NB-1
   const bf16_t* ab[4];
   const bf16_t* wb[NB];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) ab[u] = A + (int64_t)min(m0 / 16 + 4 * wave + u, last_blk) * KS32 * 512 + lane * 8;
+  for (int u = 0; u < 4; ++u)
+    ab[u] = A + ((int64_t)min(m0 / 16 + 4 * wave + u, last_blk) * KS32 + c0) * 512 + lane * 8;
 #pragma unroll
-  for (int u = 0; u < NB; ++u) wb[u] = W + (int64_t)(n0 / 16 + NB * wave + u) * KS32 * 512 + lane * 8;
+  for (int u = 0; u < NB; ++u) wb[u] = W + ((int64_t)(n0 / 16 + NB * wave + u) * KS32 + c0) * 512 + lane * 8;
   // this lane's 32x32x16 operand slot: 16-row block offset and lane slot (half 0; +32 for half 1)
   const int sub = (lane & 31) >> 4, slot = (lane & 15) + 16 * (lane >> 5);
   f32x16 acc[4][NB];
@@ -1319,7 +1339,7 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             big_store4<EPI>(e, m, n0 + 32 * NB * wn + 32 * q + 8 * j + ch, acc[p][q][4 * j], acc[p][q][4 * j + 1],
-                            acc[p][q][4 * j + 2], acc[p][q][4 * j + 3]);
+                            acc[p][q][4 * j + 2], acc[p][q][4 * j + 3], sp);
       }
     }
   }
@@ -1401,12 +1421,12 @@ static void launch_ring(const void* A, const void* W, int Mcap, const int* Mdev,
 }
 
 template <int EPI, int NB>
-static void launch_big_e(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
+static void launch_big_e(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int S, const Epi& e,
                          hipStream_t s) {
   const int ntiles = N / (64 * NB), mtiles = (Mcap + 255) / 256;
-  const int per_xcd = (ntiles * mtiles + 7) / 8;
+  const int per_xcd = S == 8 ? ntiles * mtiles : (ntiles * mtiles + 7) / 8;
   hipLaunchKernelGGL((k_gemm_big<EPI, NB>), dim3(8 * per_xcd), dim3(256), 0, s, (const bf16_t*)A, (const bf16_t*)W,
-                     Mcap, Mdev, N, K, ntiles, mtiles, per_xcd, e);
+                     Mcap, Mdev, N, K, ntiles, mtiles, per_xcd, S, e);
 }
 // 256-column tiles unless they leave CUs idle in a single partial wave of
 // workgroups and 192 divides N (n_embd-wide outputs: 1536 = 8 x 192)
@@ -1415,16 +1435,18 @@ static int big_tile_blocks(int Mcap, int N) {
   if (N % 256 == 0 && (N / 256) * mtiles >= 240) return 4;
   return N % 192 == 0 ? 3 : 4;
 }
-static void launch_big(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, const Epi& e,
-                       hipStream_t s) {
-  const bool w192 = e.mode != EPI_QKV && big_tile_blocks(Mcap, N) == 3;
-#define BIG_NB(E) (w192 ? launch_big_e<E, 3>(A, W, Mcap, Mdev, N, K, e, s) : launch_big_e<E, 4>(A, W, Mcap, Mdev, N, K, e, s))
+// nb: 32-column blocks per wave (3 or 4), 0 = by big_tile_blocks; S > 1 only with EPI_PARTIAL
+static void launch_big(const void* A, const void* W, int Mcap, const int* Mdev, int N, int K, int nb, int S,
+                       const Epi& e, hipStream_t s) {
+  const bool w192 = e.mode != EPI_QKV && (nb ? nb == 3 : big_tile_blocks(Mcap, N) == 3);
+#define BIG_NB(E) (w192 ? launch_big_e<E, 3>(A, W, Mcap, Mdev, N, K, S, e, s) : launch_big_e<E, 4>(A, W, Mcap, Mdev, N, K, S, e, s))
   switch (e.mode) {
     case EPI_STORE: BIG_NB(EPI_STORE); break;
     case EPI_ADD: BIG_NB(EPI_ADD); break;
     case EPI_RELU2: BIG_NB(EPI_RELU2); break;
     case EPI_MLPOUT: BIG_NB(EPI_MLPOUT); break;
-    case EPI_QKV: launch_big_e<EPI_QKV, 4>(A, W, Mcap, Mdev, N, K, e, s); break;
+    case EPI_PARTIAL: BIG_NB(EPI_PARTIAL); break;
+    case EPI_QKV: launch_big_e<EPI_QKV, 4>(A, W, Mcap, Mdev, N, K, 1, e, s); break;
     default: BIG_NB(EPI_SOFTCAP); break;
   }
 #undef BIG_NB
@@ -1474,6 +1496,11 @@ struct GemmPlan {
 #ifndef FC_MID_M
 #define FC_MID_M 832
 #endif
+// residual-stream GEMMs of verify chunks from FC_MID_M rows on the 256-row
+// tiles with a K split (MFMA-bound there: 1280 x 1536 x 6144 is 24 GFLOP)
+#ifndef FC_BIG_SPLIT
+#define FC_BIG_SPLIT 1
+#endif
 // Tile shape and K split by typical row count, from sweeps on MI355X at the
 // engine's shapes (N = 1536 / 4608 / 6144 / 65536, K = 1536 / 6144).
 static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
@@ -1492,6 +1519,22 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     if (tiles >= FC_BIG_MIN_TILES) {
       p.big = true;
       return p;
+    }
+  }
+  if (can_split && FC_BIG_SPLIT && Mtyp >= FC_MID_M && K % 1024 == 0) {
+    // large verify chunks (cfg5: 1152-1280 rows), residual-stream GEMMs with
+    // a deep K (the MLP c_proj): 256-row tiles with the K range split 8
+    // ways, one split per XCD, when a split's 24-32 output tiles fill that
+    // XCD's 32 CUs once; the next RMSNorm sums the partials
+    const int mt = (Mtyp + 255) / 256;
+    for (int nb = 4; nb >= 3; --nb) {
+      const int tiles = N % (64 * nb) == 0 ? mt * (N / (64 * nb)) : 0;
+      if (tiles >= 24 && tiles <= 32) {
+        p.big = true;
+        p.nb = nb;
+        p.S = 8;
+        return p;
+      }
     }
   }
   const int C = K / 64;
@@ -1640,7 +1683,7 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
                "bf16 GEMM needs K % 64 == 0 and N % 32 == 0 (fragment-order operands)");
   if (e.mode == EPI_QKV) {
     FC_CHECK_ARG(fc_gemm_fuses_qkv(Mtyp, N, K, dtype, 128), "EPI_QKV needs the 32 x 128 bf16 tile");
-    if (plan_gemm(Mtyp, N, K, dtype, false).big) launch_big(A, W, Mcap, Mdev, N, K, e, s);
+    if (plan_gemm(Mtyp, N, K, dtype, false).big) launch_big(A, W, Mcap, Mdev, N, K, 0, 1, e, s);
     else if (Mtyp >= FC_MID_M) launch_la_qkv<4>(A, W, Mcap, Mdev, N, K, e, s);  // 64 x 128 tiles
     else launch_la_qkv<2>(A, W, Mcap, Mdev, N, K, e, s);
     FC_LAUNCH_CHECK();
@@ -1664,9 +1707,8 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   if (p.gemv) {
     launch_gemv<float>(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.big) {
-    FC_CHECK_ARG(ee.mode != EPI_PARTIAL && ee.rms_in == nullptr && ee.xa == nullptr,
-                 "the 256 x 256 GEMM has no split-K or folded-norm epilogue");
-    launch_big(A, W, Mcap, Mdev, N, K, ee, s);
+    FC_CHECK_ARG(ee.rms_in == nullptr && ee.xa == nullptr, "the 256 x 256 GEMM has no folded-norm epilogue");
+    launch_big(A, W, Mcap, Mdev, N, K, p.nb, p.S, ee, s);
   } else if (p.ring) {
     if (p.mb == 2) launch_ring<2, 2, 4, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);  // 32 x 32, 4 stages
     else launch_ring<4, 6, 5, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);           // 64 x 96, 5 stages

@@ -147,3 +147,24 @@ def test_full_forward_bf16_verify_size_split():
     err = float(np.abs(got - ref).max())
     _say(f"  max abs err {err:.3e}")
     assert err < 2e-2
+
+
+def test_full_forward_bf16_large_verify_split_big_tiles():
+    """n_embd 1536 at 8 x 150 tokens (M = 1200, a large-batch verify chunk
+    like cfg5's 128 rows x 9-10 tokens): the MLP c_proj (K = 6144) takes the
+    256 x 256 tiles with an 8-way K split, one split per XCD (30 tiles x 8 =
+    240 workgroups), whose partials the RMSNorm kernel sums with the
+    residual / lambda / backout update (the second layer is the last:
+    backout applied there)."""
+    from flaxchat_amd.config import GPTConfig
+    from flaxchat_amd.gpt import GPT
+    _say("full forward bf16 d1536 8 x 150 (split 256-row tiles)")
+    cfg = GPTConfig(sequence_len=256, vocab_size=1024, n_layer=2, n_head=12, n_kv_head=12, n_embd=1536,
+                    window_pattern="SL", short_window=64)
+    m = GPT.init_normal(cfg, seed=15, std=0.02).perturb_scalars()
+    ids = np.random.default_rng(15).integers(0, cfg.vocab_size, (8, 150))
+    got = gpt_forward(m, ids, dtype="bf16", chunk=150).cpu().numpy()
+    ref = gpt_call(m, ids)
+    err = float(np.abs(got - ref).max())
+    _say(f"  max abs err {err:.3e}")
+    assert err < 2e-2
