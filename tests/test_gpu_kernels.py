@@ -45,7 +45,7 @@ def _gemm_cases():
     epilogue checks."""
     cases = []
     for NK in [(256, 384), (1536, 6144)]:
-        for M in [1, 3, 5, 16, 32, 64, 100, 224, 300]:
+        for M in [1, 3, 5, 16, 32, 40, 64, 100, 224, 300]:
             for epi in [0, 1, 2, 4]:
                 for dtype in ["fp32", "bf16"]:
                     big = NK[0] * NK[1] > 1e6
