@@ -200,6 +200,50 @@ def walk_ceiling(dev, units, n_bytes, n_rep=5, n_buf=3):
     return res
 
 
+# The cfg4 verify GEMMs (224 packed tokens) at the tilings the engine's plan
+# gives them: (name, M, N, K, tile_m, tile_n, K splits)
+VERIFY_GEMM_TILINGS = [("qkv_32x128", 224, 4608, 1536, 32, 128, 1),
+                       ("attn_cproj_32x32", 224, 1536, 1536, 32, 32, 1),
+                       ("c_fc_64x64", 224, 6144, 1536, 64, 64, 1),
+                       ("mlp_cproj_64x96_split4", 224, 1536, 6144, 64, 96, 4)]
+
+
+def gemm_walks(dev, n_rep=4, pool_bytes=320 << 20):
+    """The verify GEMMs' operand walks without their arithmetic
+    (fc_gemm_walk_probe) at the engine's tilings: the activation operand
+    L2-resident (one buffer, as its producer just wrote it), the weights
+    cycled over copies filling `pool_bytes` so every launch reads them from
+    HBM, as in a round. {name: {"us": per launch, "l2_to_cu_mb": the bytes
+    the CUs read}}."""
+    import torch
+    from flaxchat_amd import _lib
+    pool = torch.ones(pool_bytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream(dev)
+    res = {}
+    for name, M, N, K, tm, tn, S in VERIFY_GEMM_TILINGS:
+        a = torch.ones((M + 15) // 16 * 16 * K * 2, dtype=torch.uint8, device=dev)
+        wb = N * K * 2
+        n_copies = pool_bytes // wb
+        out = torch.empty(_lib.lib().fc_gemm_walk_probe_words(M, N, tm, tn, S), dtype=torch.int32, device=dev)
+        run = lambda i: _lib.check(_lib.lib().fc_gemm_walk_probe(  # noqa: E731
+            a.data_ptr(), pool.data_ptr() + (i % n_copies) * wb, M, N, K, tm, tn, S, out.data_ptr(),
+            s.cuda_stream), "fc_gemm_walk_probe")
+        for i in range(n_copies):
+            run(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(n_rep * n_copies):
+            run(i)
+        e1.record(s)
+        e1.synchronize()
+        mt = (M + tm - 1) // tm
+        l2b = mt * (N // tn) * K * 2 * (tm + tn)
+        res[name] = {"us": round(e0.elapsed_time(e1) * 1e3 / (n_rep * n_copies), 2), "l2_to_cu_mb": round(l2b / 1e6, 1)}
+        del a, out
+    del pool
+    return res
+
+
 def l2_ceiling(dev, region=1 << 20, n_bytes=1 << 30, n_rep=5, grids=(256, 512, 1024)):
     """Measured L2-to-CU read ceiling: fc_l2_read_probe (each XCD's workgroups
     read a 1 MB region that stays in that XCD's L2, direct-to-LDS loads)
@@ -422,6 +466,8 @@ def main():
         l2c = l2_ceiling(target.device)
         # the attention's own grid and tile walk without its compute
         wceil = walk_ceiling(target.device, sess.B * sess.T.G, int(r["per_launch_bytes"]))
+        # the verify GEMMs' operand walks at their tilings (cfg4 shapes)
+        gwalks = gemm_walks(target.device) if args.config == "cfg4" else None
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
@@ -433,7 +479,8 @@ def main():
                 "read_ceiling_launch_bytes": round(rceil_l, 1),
                 "frac_of_read_ceiling_launch_bytes": round(r["achieved"] / rceil_l, 4),
                 "walk_ceiling": round(wceil, 1), "frac_of_walk_ceiling": round(r["achieved"] / wceil, 4),
-                "l2_read_ceiling_by_workgroups": l2c}
+                "l2_read_ceiling_by_workgroups": l2c,
+                "gemm_walks": gwalks}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
               f"1 GiB streaming read: {rceil:.0f} GB/s, streaming read of one launch's "
               f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s; its own load walk: {wceil:.0f} GB/s; "

@@ -69,8 +69,8 @@ EXPORTS = ["fc_last_error", "fc_version", "fc_forward_workspace_bytes", "fc_forw
            "fc_attention_workspace_bytes", "fc_attention", "fc_attention_noalloc", "fc_attention_noalloc_max_bytes",
            "fc_attn_prologue", "fc_attn_qkv_workspace_bytes", "fc_attn_qkv", "fc_row_stats", "fc_spec_workspace_bytes",
            "fc_spec_round", "fc_spec_accept", "fc_spec_part_bytes", "fc_fast_sample", "fc_engine_sample",
-           "fc_cross_entropy", "fc_read_probe", "fc_l2_read_probe", "fc_walk_probe",
-           "fc_graph_begin", "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
+           "fc_cross_entropy", "fc_read_probe", "fc_l2_read_probe", "fc_walk_probe", "fc_gemm_walk_probe",
+           "fc_gemm_walk_probe_words", "fc_graph_begin", "fc_graph_end", "fc_graph_launch", "fc_graph_destroy"]
 
 _lib = None
 
@@ -124,6 +124,10 @@ def _declare(L):
     L.fc_l2_read_probe.restype = i32
     L.fc_walk_probe.argtypes = [vp, i32, i32, vp, vp]
     L.fc_walk_probe.restype = i32
+    L.fc_gemm_walk_probe.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    L.fc_gemm_walk_probe.restype = i32
+    L.fc_gemm_walk_probe_words.argtypes = [i32, i32, i32, i32, i32]
+    L.fc_gemm_walk_probe_words.restype = i32
     L.fc_graph_begin.argtypes = [vp]
     L.fc_graph_begin.restype = i32
     L.fc_graph_end.argtypes = [vp, POINTER(c_void_p)]

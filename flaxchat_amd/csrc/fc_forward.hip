@@ -719,3 +719,71 @@ extern "C" int32_t fc_walk_probe(const void* src, int32_t units, int32_t tiles, 
   FC_LAUNCH_CHECK();
   return FC_OK;
 }
+
+// A GEMM's operand walk without its arithmetic: the blocks the K-split,
+// LDS-shared and ring kernels read, in their order, timed by the benchmark
+// against the GEMMs themselves. Operands in fragment order (1 KB blocks of
+// 16 rows x 32 k, [row block][k step]); output tile (mt, nt) of tile_m x
+// tile_n and K split s; XCD x takes the grid's tiles [x per_xcd, (x + 1)
+// per_xcd), M tile fastest (the M tiles that share a weight slab on one
+// XCD). Wave w takes the k steps w, w + 4, ... of the split's range and per
+// k step loads the tile's A blocks (row blocks past the last live one
+// clamped, as the kernels do) then its W blocks, each a 1 KB direct
+// global-to-LDS load, at most GWP_DEPTH in flight, no barrier. Output word
+// of a wave: the XOR over lanes and words of the LDS slots its last
+// min(loads, 16) loads landed in.
+#define GWP_DEPTH 16
+__global__ __launch_bounds__(256) void k_gemm_walk_probe(const char* __restrict__ A, const char* __restrict__ W,
+                                                         int M, int KS, int mb, int nb, int mtiles, int ntiles,
+                                                         int S, int per_xcd, uint32_t* __restrict__ out) {
+  __shared__ uint4 ring[4][16][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= per_xcd || t >= mtiles * ntiles * S) return;
+  const int mt = t % mtiles, rest = t / mtiles, sp = rest % S, nt = rest / S;
+  const int k0 = (int)((int64_t)sp * KS / S), k1 = (int)((int64_t)(sp + 1) * KS / S);
+  const int last_blk = (M - 1) >> 4;
+  int cnt = 0;
+  for (int ks = k0 + wave; ks < k1; ks += 4) {
+    for (int b = 0; b < mb + nb; ++b) {
+      const int64_t blk = b < mb ? (int64_t)min(mt * mb + b, last_blk) * KS + ks
+                                 : (int64_t)(nt * nb + b - mb) * KS + ks;
+      __builtin_amdgcn_global_load_lds((const void*)((b < mb ? A : W) + blk * 1024 + lane * 16),
+                                       (__attribute__((address_space(3))) void*)&ring[wave][cnt & 15][0], 16, 0, 0);
+      ++cnt;
+      __builtin_amdgcn_s_waitcnt(((GWP_DEPTH - 1) & 15) | (((GWP_DEPTH - 1) >> 4) << 14) | (7 << 4) | (15 << 8));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in its own slots
+  uint32_t x = 0u;
+  for (int j = 0; j < min(cnt, 16); ++j) {
+    const uint4 v = ring[wave][j][lane];
+    x ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o, WAVE);
+  if (lane == 0) out[blockIdx.x * 4 + wave] = x;
+}
+
+extern "C" int32_t fc_gemm_walk_probe_words(int32_t M, int32_t N, int32_t tile_m, int32_t tile_n, int32_t splits) {
+  if (M <= 0 || N <= 0 || tile_m <= 0 || tile_n <= 0 || splits <= 0) return -1;
+  const int64_t tiles = (int64_t)((M + tile_m - 1) / tile_m) * (N / tile_n) * splits;
+  return (int32_t)(4 * 8 * ((tiles + 7) / 8));
+}
+
+extern "C" int32_t fc_gemm_walk_probe(const void* A, const void* W, int32_t M, int32_t N, int32_t K, int32_t tile_m,
+                                      int32_t tile_n, int32_t splits, uint32_t* out, void* stream) {
+  FC_CHECK_ARG(A && W && out, "null pointer");
+  FC_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 32 == 0, "M, N > 0 and K a positive multiple of 32");
+  FC_CHECK_ARG(tile_m > 0 && tile_m % 16 == 0 && tile_n > 0 && tile_n % 16 == 0 && N % tile_n == 0,
+               "tiles: multiples of 16, tile_n dividing N");
+  FC_CHECK_ARG(splits >= 1 && splits <= K / 32, "splits in [1, K / 32]");
+  const int mtiles = (M + tile_m - 1) / tile_m, ntiles = N / tile_n;
+  const int64_t tiles = (int64_t)mtiles * ntiles * splits;
+  FC_CHECK_ARG(tiles <= (1 << 20), "at most 2^20 tiles");
+  const int per_xcd = (int)((tiles + 7) / 8);
+  hipLaunchKernelGGL(k_gemm_walk_probe, dim3(8 * per_xcd), dim3(256), 0, (hipStream_t)stream, (const char*)A,
+                     (const char*)W, M, K / 32, tile_m / 16, tile_n / 16, mtiles, ntiles, splits, per_xcd, out);
+  FC_LAUNCH_CHECK();
+  return FC_OK;
+}

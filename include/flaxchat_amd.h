@@ -344,6 +344,21 @@ int32_t fc_l2_read_probe(const void* src, int64_t region_bytes, int64_t bytes, u
  * attention can reach with its grid and tile walk. */
 int32_t fc_walk_probe(const void* src, int32_t units, int32_t tiles, uint32_t* out, void* stream);
 
+/* A GEMM's operand walk without its arithmetic: for output tiles of
+ * tile_m x tile_n (multiples of 16; tile_n divides N) and a K split of
+ * `splits`, each workgroup loads its tile's 1 KB fragment-order blocks of A
+ * (round16(M) x K) and W (N x K) over its split's k steps, four waves taking
+ * every fourth k step, with direct global-to-LDS loads (16 in flight per
+ * wave, no barrier), the M tiles that share a weight slab on one XCD, as
+ * the K-split, LDS-shared and ring GEMM kernels read them. `out` receives
+ * fc_gemm_walk_probe_words(M, N, tile_m, tile_n, splits) words (the XOR of
+ * each wave's last 16 landed blocks; untouched for workgroups past the
+ * tiles). No counterpart in the reference: the rate a GEMM of that tiling
+ * can reach whatever its MFMA work and epilogue. */
+int32_t fc_gemm_walk_probe(const void* A, const void* W, int32_t M, int32_t N, int32_t K, int32_t tile_m,
+                           int32_t tile_n, int32_t splits, uint32_t* out, void* stream);
+int32_t fc_gemm_walk_probe_words(int32_t M, int32_t N, int32_t tile_m, int32_t tile_n, int32_t splits);
+
 /* Stream capture into a replayable hipGraph (the captured draft loop). */
 int32_t fc_graph_begin(void* stream);
 int32_t fc_graph_end(void* stream, void** exec_out);

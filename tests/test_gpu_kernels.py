@@ -691,6 +691,55 @@ def test_walk_probe_reads_each_units_tiles():
     assert _lib.lib().fc_walk_probe(src.data_ptr(), 0, tiles, out.data_ptr(), stream()) != 0  # refused
 
 
+def test_gemm_walk_probe_reads_each_tiles_blocks():
+    """fc_gemm_walk_probe (the GEMM operand walk bench.py times): workgroup g
+    takes tile t = (g % 8) per_xcd + g / 8, decoded M tile fastest, then K
+    split, then N tile; wave w walks the split's k steps w, w + 4, ..., per k
+    step the tile's A blocks (row blocks clamped to the last live one) then
+    its W blocks. Its word is the XOR of the last min(loads, 16) blocks it
+    landed (each lane's 16 bytes, every word), recomputed here for a ragged
+    M, three N tiles and two K splits."""
+    M, N, K, tm, tn, S = 40, 96, 256, 32, 32, 2
+    KS, mb, nb = K // 32, tm // 16, tn // 16
+    mtiles, ntiles = (M + tm - 1) // tm, N // tn
+    rng = np.random.default_rng(47)
+    a_words = rng.integers(0, 2**32, ((M + 15) // 16) * KS * 256, dtype=np.uint64).astype(np.uint32)
+    w_words = rng.integers(0, 2**32, (N // 16) * KS * 256, dtype=np.uint64).astype(np.uint32)
+    A = torch.from_numpy(a_words.view(np.int32)).to(dev())
+    W = torch.from_numpy(w_words.view(np.int32)).to(dev())
+    nwords = _lib.lib().fc_gemm_walk_probe_words(M, N, tm, tn, S)
+    out = torch.zeros(nwords, dtype=torch.int32, device=dev())
+    check(_lib.lib().fc_gemm_walk_probe(A.data_ptr(), W.data_ptr(), M, N, K, tm, tn, S, out.data_ptr(), stream()),
+          "fc_gemm_walk_probe")
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32).reshape(-1, 4)
+    blk_xor = lambda words, i: np.bitwise_xor.reduce(words[i * 256:(i + 1) * 256])  # noqa: E731
+    tiles = mtiles * ntiles * S
+    per_xcd = (tiles + 7) // 8
+    want = np.zeros((8 * per_xcd, 4), np.uint32)
+    last_blk = (M - 1) // 16
+    for g in range(8 * per_xcd):
+        t = (g % 8) * per_xcd + g // 8
+        if g // 8 >= per_xcd or t >= tiles:
+            continue
+        mt, rest = t % mtiles, t // mtiles
+        sp, nt = rest % S, rest // S
+        k0, k1 = sp * KS // S, (sp + 1) * KS // S
+        for w in range(4):
+            seq = []
+            for ks in range(k0 + w, k1, 4):
+                for b in range(mb + nb):
+                    if b < mb:
+                        seq.append(blk_xor(a_words, min(mt * mb + b, last_blk) * KS + ks))
+                    else:
+                        seq.append(blk_xor(w_words, (nt * nb + b - mb) * KS + ks))
+            x = np.uint32(0)
+            for v in seq[-16:]:
+                x ^= v
+            want[g, w] = x
+    assert np.array_equal(got, want)
+
+
 def test_l2_read_probe_reads_its_region():
     """fc_l2_read_probe (the L2-to-CU ceiling bench.py reports): workgroup w
     walks 4 KB steps through the region of XCD w % 8 from offset
