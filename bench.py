@@ -200,45 +200,53 @@ def walk_ceiling(dev, units, n_bytes, n_rep=5, n_buf=3):
     return res
 
 
-# The cfg4 verify GEMMs (224 packed tokens) at the tilings the engine's plan
-# gives them: (name, M, N, K, tile_m, tile_n, K splits)
-VERIFY_GEMM_TILINGS = [("qkv_32x128", 224, 4608, 1536, 32, 128, 1),
-                       ("attn_cproj_32x32", 224, 1536, 1536, 32, 32, 1),
-                       ("c_fc_64x64", 224, 6144, 1536, 64, 64, 1),
-                       ("mlp_cproj_64x96_split4", 224, 1536, 6144, 64, 96, 4)]
+# The cfg4 verify GEMMs (224 packed tokens) and draft-step GEMMs (32 rows)
+# at the tilings the engine's plan gives them: (name, M, N, K, tile_m,
+# tile_n, K splits)
+GEMM_TILINGS = [("verify_qkv_32x128", 224, 4608, 1536, 32, 128, 1),
+                ("verify_attn_cproj_32x32", 224, 1536, 1536, 32, 32, 1),
+                ("verify_c_fc_64x64", 224, 6144, 1536, 64, 64, 1),
+                ("verify_mlp_cproj_64x96_split4", 224, 1536, 6144, 64, 96, 4),
+                ("draft_qkv_32x32", 32, 4608, 1536, 32, 32, 1),
+                ("draft_attn_cproj_32x16", 32, 1536, 1536, 32, 16, 1),
+                ("draft_c_fc_32x32", 32, 6144, 1536, 32, 32, 1),
+                ("draft_mlp_cproj_32x16_split8", 32, 1536, 6144, 32, 16, 8),
+                ("draft_lm_head_32x64", 32, 65536, 1536, 32, 64, 1)]
 
 
-def gemm_walks(dev, n_rep=4, pool_bytes=320 << 20):
-    """The verify GEMMs' operand walks without their arithmetic
-    (fc_gemm_walk_probe) at the engine's tilings: the activation operand
-    L2-resident (one buffer, as its producer just wrote it), the weights
-    cycled over copies filling `pool_bytes` so every launch reads them from
-    HBM, as in a round. {name: {"us": per launch, "l2_to_cu_mb": the bytes
-    the CUs read}}."""
+def gemm_walks(dev, n_rep=4, pool_bytes=640 << 20):
+    """The cfg4 GEMMs' operand walks without their arithmetic
+    (fc_gemm_walk_probe) at the engine's tilings, with direct-to-LDS loads
+    and with register loads: the activation operand L2-resident (one buffer,
+    as its producer just wrote it), the weights cycled over copies filling
+    `pool_bytes` so every launch reads them from HBM, as in a round.
+    {name: {"lds_us", "reg_us": per launch, "l2_to_cu_mb": the bytes the
+    CUs read}}."""
     import torch
     from flaxchat_amd import _lib
     pool = torch.ones(pool_bytes, dtype=torch.uint8, device=dev)
     s = torch.cuda.current_stream(dev)
     res = {}
-    for name, M, N, K, tm, tn, S in VERIFY_GEMM_TILINGS:
+    for name, M, N, K, tm, tn, S in GEMM_TILINGS:
         a = torch.ones((M + 15) // 16 * 16 * K * 2, dtype=torch.uint8, device=dev)
         wb = N * K * 2
         n_copies = pool_bytes // wb
         out = torch.empty(_lib.lib().fc_gemm_walk_probe_words(M, N, tm, tn, S), dtype=torch.int32, device=dev)
-        run = lambda i: _lib.check(_lib.lib().fc_gemm_walk_probe(  # noqa: E731
-            a.data_ptr(), pool.data_ptr() + (i % n_copies) * wb, M, N, K, tm, tn, S, out.data_ptr(),
-            s.cuda_stream), "fc_gemm_walk_probe")
-        for i in range(n_copies):
-            run(i)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for i in range(n_rep * n_copies):
-            run(i)
-        e1.record(s)
-        e1.synchronize()
         mt = (M + tm - 1) // tm
-        l2b = mt * (N // tn) * K * 2 * (tm + tn)
-        res[name] = {"us": round(e0.elapsed_time(e1) * 1e3 / (n_rep * n_copies), 2), "l2_to_cu_mb": round(l2b / 1e6, 1)}
+        res[name] = {"l2_to_cu_mb": round(mt * (N // tn) * K * 2 * (tm + tn) / 1e6, 1)}
+        for key, reg in (("lds_us", 0), ("reg_us", 1)):
+            run = lambda i: _lib.check(_lib.lib().fc_gemm_walk_probe(  # noqa: E731
+                a.data_ptr(), pool.data_ptr() + (i % n_copies) * wb, M, N, K, tm, tn, S, reg, out.data_ptr(),
+                s.cuda_stream), "fc_gemm_walk_probe")
+            for i in range(n_copies):
+                run(i)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(n_rep * n_copies):
+                run(i)
+            e1.record(s)
+            e1.synchronize()
+            res[name][key] = round(e0.elapsed_time(e1) * 1e3 / (n_rep * n_copies), 2)
         del a, out
     del pool
     return res
@@ -466,7 +474,7 @@ def main():
         l2c = l2_ceiling(target.device)
         # the attention's own grid and tile walk without its compute
         wceil = walk_ceiling(target.device, sess.B * sess.T.G, int(r["per_launch_bytes"]))
-        # the verify GEMMs' operand walks at their tilings (cfg4 shapes)
+        # the GEMMs' operand walks at their tilings (cfg4 shapes)
         gwalks = gemm_walks(target.device) if args.config == "cfg4" else None
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),

@@ -124,7 +124,7 @@ def _declare(L):
     L.fc_l2_read_probe.restype = i32
     L.fc_walk_probe.argtypes = [vp, i32, i32, vp, vp]
     L.fc_walk_probe.restype = i32
-    L.fc_gemm_walk_probe.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    L.fc_gemm_walk_probe.argtypes = [vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp]
     L.fc_gemm_walk_probe.restype = i32
     L.fc_gemm_walk_probe_words.argtypes = [i32, i32, i32, i32, i32]
     L.fc_gemm_walk_probe_words.restype = i32

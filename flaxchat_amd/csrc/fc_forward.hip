@@ -726,39 +726,63 @@ extern "C" int32_t fc_walk_probe(const void* src, int32_t units, int32_t tiles, 
 // 16 rows x 32 k, [row block][k step]); output tile (mt, nt) of tile_m x
 // tile_n and K split s; XCD x takes the grid's tiles [x per_xcd, (x + 1)
 // per_xcd), M tile fastest (the M tiles that share a weight slab on one
-// XCD). Wave w takes the k steps w, w + 4, ... of the split's range and per
-// k step loads the tile's A blocks (row blocks past the last live one
-// clamped, as the kernels do) then its W blocks, each a 1 KB direct
-// global-to-LDS load, at most GWP_DEPTH in flight, no barrier. Output word
-// of a wave: the XOR over lanes and words of the LDS slots its last
-// min(loads, 16) loads landed in.
+// XCD). The split's range is cut into 64-deep k chunks (two k steps), as
+// the kernels cut it; wave w takes chunks w, w + 4, ... and per chunk loads
+// the tile's W blocks then its A blocks (row blocks past the last live one
+// clamped, as the kernels do), each block's two k steps back to back (2 KB
+// contiguous), 1 KB per load instruction (16 bytes per lane), at most
+// GWP_DEPTH in flight, no barrier.
+//   REG = false: direct global-to-LDS loads (k_gemm_dma, k_gemm_ring); the
+//     wave's word is the XOR over lanes and words of the LDS slots its last
+//     min(loads, 16) loads landed in.
+//   REG = true: loads into registers, GWP_DEPTH issued then consumed
+//     (k_gemm_ks, k_gemm_la's weights); the wave's word is the XOR of every
+//     block it loaded.
 #define GWP_DEPTH 16
+template <bool REG>
 __global__ __launch_bounds__(256) void k_gemm_walk_probe(const char* __restrict__ A, const char* __restrict__ W,
                                                          int M, int KS, int mb, int nb, int mtiles, int ntiles,
                                                          int S, int per_xcd, uint32_t* __restrict__ out) {
-  __shared__ uint4 ring[4][16][64];
+  __shared__ uint4 ring[REG ? 1 : 4][16][64];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if ((int)(blockIdx.x >> 3) >= per_xcd || t >= mtiles * ntiles * S) return;
   const int mt = t % mtiles, rest = t / mtiles, sp = rest % S, nt = rest / S;
-  const int k0 = (int)((int64_t)sp * KS / S), k1 = (int)((int64_t)(sp + 1) * KS / S);
+  const int C = KS >> 1;  // 64-deep chunks
+  const int c0 = (int)((int64_t)sp * C / S), c1 = (int)((int64_t)(sp + 1) * C / S);
   const int last_blk = (M - 1) >> 4;
-  int cnt = 0;
-  for (int ks = k0 + wave; ks < k1; ks += 4) {
-    for (int b = 0; b < mb + nb; ++b) {
-      const int64_t blk = b < mb ? (int64_t)min(mt * mb + b, last_blk) * KS + ks
-                                 : (int64_t)(nt * nb + b - mb) * KS + ks;
-      __builtin_amdgcn_global_load_lds((const void*)((b < mb ? A : W) + blk * 1024 + lane * 16),
-                                       (__attribute__((address_space(3))) void*)&ring[wave][cnt & 15][0], 16, 0, 0);
-      ++cnt;
+  const int per_c = 2 * (mb + nb);
+  // the wave's loads in order: load j is chunk c0 + wave + 4 (j / per_c);
+  // within it, u = j % per_c: block u / 2 (W blocks first), k step 2 c + u % 2
+  const int nch = c1 - c0 > wave ? (c1 - c0 - wave + 3) >> 2 : 0;
+  const int nload = nch * per_c;
+  auto addr = [&](int j) {
+    const int c = c0 + wave + 4 * (j / per_c), u = j % per_c, b = u >> 1, ks = 2 * c + (u & 1);
+    const int64_t blk = b < nb ? (int64_t)(nt * nb + b) * KS + ks
+                               : (int64_t)min(mt * mb + b - nb, last_blk) * KS + ks;
+    return (b < nb ? W : A) + blk * 1024 + lane * 16;
+  };
+  uint32_t x = 0u;
+  if constexpr (REG) {
+    for (int j0 = 0; j0 < nload; j0 += GWP_DEPTH) {
+      uint4 r[GWP_DEPTH];
+#pragma unroll
+      for (int u = 0; u < GWP_DEPTH; ++u) r[u] = *(const uint4*)addr(min(j0 + u, nload - 1));
+#pragma unroll
+      for (int u = 0; u < GWP_DEPTH; ++u)
+        if (j0 + u < nload) x ^= r[u].x ^ r[u].y ^ r[u].z ^ r[u].w;
+    }
+  } else {
+    for (int j = 0; j < nload; ++j) {
+      __builtin_amdgcn_global_load_lds((const void*)addr(j),
+                                       (__attribute__((address_space(3))) void*)&ring[wave][j & 15][0], 16, 0, 0);
       __builtin_amdgcn_s_waitcnt(((GWP_DEPTH - 1) & 15) | (((GWP_DEPTH - 1) >> 4) << 14) | (7 << 4) | (15 << 8));
     }
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in its own slots
-  uint32_t x = 0u;
-  for (int j = 0; j < min(cnt, 16); ++j) {
-    const uint4 v = ring[wave][j][lane];
-    x ^= v.x ^ v.y ^ v.z ^ v.w;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in its own slots
+    for (int j = 0; j < min(nload, 16); ++j) {
+      const uint4 v = ring[wave][j][lane];
+      x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o, WAVE);
@@ -772,18 +796,24 @@ extern "C" int32_t fc_gemm_walk_probe_words(int32_t M, int32_t N, int32_t tile_m
 }
 
 extern "C" int32_t fc_gemm_walk_probe(const void* A, const void* W, int32_t M, int32_t N, int32_t K, int32_t tile_m,
-                                      int32_t tile_n, int32_t splits, uint32_t* out, void* stream) {
+                                      int32_t tile_n, int32_t splits, int32_t reg_loads, uint32_t* out, void* stream) {
   FC_CHECK_ARG(A && W && out, "null pointer");
-  FC_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 32 == 0, "M, N > 0 and K a positive multiple of 32");
+  FC_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 64 == 0, "M, N > 0 and K a positive multiple of 64");
   FC_CHECK_ARG(tile_m > 0 && tile_m % 16 == 0 && tile_n > 0 && tile_n % 16 == 0 && N % tile_n == 0,
                "tiles: multiples of 16, tile_n dividing N");
-  FC_CHECK_ARG(splits >= 1 && splits <= K / 32, "splits in [1, K / 32]");
+  FC_CHECK_ARG(splits >= 1 && splits <= K / 64, "splits in [1, K / 64]");
   const int mtiles = (M + tile_m - 1) / tile_m, ntiles = N / tile_n;
   const int64_t tiles = (int64_t)mtiles * ntiles * splits;
   FC_CHECK_ARG(tiles <= (1 << 20), "at most 2^20 tiles");
   const int per_xcd = (int)((tiles + 7) / 8);
-  hipLaunchKernelGGL(k_gemm_walk_probe, dim3(8 * per_xcd), dim3(256), 0, (hipStream_t)stream, (const char*)A,
-                     (const char*)W, M, K / 32, tile_m / 16, tile_n / 16, mtiles, ntiles, splits, per_xcd, out);
+  if (reg_loads)
+    hipLaunchKernelGGL(k_gemm_walk_probe<true>, dim3(8 * per_xcd), dim3(256), 0, (hipStream_t)stream,
+                       (const char*)A, (const char*)W, M, K / 32, tile_m / 16, tile_n / 16, mtiles, ntiles, splits,
+                       per_xcd, out);
+  else
+    hipLaunchKernelGGL(k_gemm_walk_probe<false>, dim3(8 * per_xcd), dim3(256), 0, (hipStream_t)stream,
+                       (const char*)A, (const char*)W, M, K / 32, tile_m / 16, tile_n / 16, mtiles, ntiles, splits,
+                       per_xcd, out);
   FC_LAUNCH_CHECK();
   return FC_OK;
 }

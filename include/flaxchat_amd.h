@@ -345,18 +345,21 @@ int32_t fc_l2_read_probe(const void* src, int64_t region_bytes, int64_t bytes, u
 int32_t fc_walk_probe(const void* src, int32_t units, int32_t tiles, uint32_t* out, void* stream);
 
 /* A GEMM's operand walk without its arithmetic: for output tiles of
- * tile_m x tile_n (multiples of 16; tile_n divides N) and a K split of
- * `splits`, each workgroup loads its tile's 1 KB fragment-order blocks of A
- * (round16(M) x K) and W (N x K) over its split's k steps, four waves taking
- * every fourth k step, with direct global-to-LDS loads (16 in flight per
- * wave, no barrier), the M tiles that share a weight slab on one XCD, as
- * the K-split, LDS-shared and ring GEMM kernels read them. `out` receives
- * fc_gemm_walk_probe_words(M, N, tile_m, tile_n, splits) words (the XOR of
- * each wave's last 16 landed blocks; untouched for workgroups past the
- * tiles). No counterpart in the reference: the rate a GEMM of that tiling
- * can reach whatever its MFMA work and epilogue. */
+ * tile_m x tile_n (multiples of 16; tile_n divides N), K a multiple of 64
+ * and a K split of `splits` (at most K / 64), each workgroup loads its
+ * tile's 1 KB fragment-order blocks of W (N x K) and A (round16(M) x K)
+ * over its split's 64-deep k chunks, four waves taking every fourth chunk,
+ * 16 loads of 1 KB in flight per wave and no barrier,
+ * the M tiles that share a weight slab on one XCD, as the K-split,
+ * LDS-shared and ring GEMM kernels read them: with direct global-to-LDS
+ * loads (reg_loads = 0; each wave's word is the XOR of its last 16 landed
+ * blocks) or loads into registers (reg_loads = 1; the XOR of every block it
+ * loaded). `out` receives fc_gemm_walk_probe_words(M, N, tile_m, tile_n,
+ * splits) words (untouched for workgroups past the tiles). No counterpart
+ * in the reference: the rate a GEMM of that tiling can reach whatever its
+ * MFMA work and epilogue. */
 int32_t fc_gemm_walk_probe(const void* A, const void* W, int32_t M, int32_t N, int32_t K, int32_t tile_m,
-                           int32_t tile_n, int32_t splits, uint32_t* out, void* stream);
+                           int32_t tile_n, int32_t splits, int32_t reg_loads, uint32_t* out, void* stream);
 int32_t fc_gemm_walk_probe_words(int32_t M, int32_t N, int32_t tile_m, int32_t tile_n, int32_t splits);
 
 /* Stream capture into a replayable hipGraph (the captured draft loop). */

@@ -62,11 +62,11 @@ def test_argument_errors_are_status_codes():
     assert L.fc_walk_probe(None, 4, 2, p, None) == -1 and b"null" in L.fc_last_error()
     assert L.fc_walk_probe(p, 0, 2, p, None) == -1
     assert L.fc_walk_probe(p, 4, 0, p, None) == -1
-    assert L.fc_gemm_walk_probe(None, p, 32, 64, 256, 32, 32, 1, p, None) == -1 and b"null" in L.fc_last_error()
-    assert L.fc_gemm_walk_probe(p, p, 32, 64, 250, 32, 32, 1, p, None) == -1  # K not a multiple of 32
-    assert L.fc_gemm_walk_probe(p, p, 32, 64, 256, 32, 48, 1, p, None) == -1  # tile_n does not divide N
-    assert L.fc_gemm_walk_probe(p, p, 32, 64, 256, 24, 32, 1, p, None) == -1  # tile_m not a multiple of 16
-    assert L.fc_gemm_walk_probe(p, p, 32, 64, 256, 32, 32, 9, p, None) == -1  # more splits than k steps
+    assert L.fc_gemm_walk_probe(None, p, 32, 64, 256, 32, 32, 1, 0, p, None) == -1 and b"null" in L.fc_last_error()
+    assert L.fc_gemm_walk_probe(p, p, 32, 64, 288, 32, 32, 1, 0, p, None) == -1  # K not a multiple of 64
+    assert L.fc_gemm_walk_probe(p, p, 32, 64, 256, 32, 48, 1, 0, p, None) == -1  # tile_n does not divide N
+    assert L.fc_gemm_walk_probe(p, p, 32, 64, 256, 24, 32, 1, 0, p, None) == -1  # tile_m not a multiple of 16
+    assert L.fc_gemm_walk_probe(p, p, 32, 64, 256, 32, 32, 5, 0, p, None) == -1  # more splits than 64-deep chunks
     assert L.fc_gemm_walk_probe_words(224, 4608, 32, 128, 1) == 4 * 8 * 32  # 252 tiles -> 8 x 32 workgroups
     assert L.fc_gemm_walk_probe_words(0, 64, 32, 32, 1) == -1
 

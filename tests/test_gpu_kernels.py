@@ -691,15 +691,18 @@ def test_walk_probe_reads_each_units_tiles():
     assert _lib.lib().fc_walk_probe(src.data_ptr(), 0, tiles, out.data_ptr(), stream()) != 0  # refused
 
 
-def test_gemm_walk_probe_reads_each_tiles_blocks():
+@pytest.mark.parametrize("reg_loads", [0, 1])
+def test_gemm_walk_probe_reads_each_tiles_blocks(reg_loads):
     """fc_gemm_walk_probe (the GEMM operand walk bench.py times): workgroup g
     takes tile t = (g % 8) per_xcd + g / 8, decoded M tile fastest, then K
-    split, then N tile; wave w walks the split's k steps w, w + 4, ..., per k
-    step the tile's A blocks (row blocks clamped to the last live one) then
-    its W blocks. Its word is the XOR of the last min(loads, 16) blocks it
-    landed (each lane's 16 bytes, every word), recomputed here for a ragged
-    M, three N tiles and two K splits."""
-    M, N, K, tm, tn, S = 40, 96, 256, 32, 32, 2
+    split, then N tile; wave w walks the split's 64-deep k chunks w, w + 4,
+    ..., per chunk the tile's W blocks then its A blocks (row blocks clamped
+    to the last live one), each block's two k steps in turn. Its word is
+    the XOR (each lane's 16 bytes, every word) of the last min(loads, 16)
+    blocks it landed in LDS (direct loads) or of every block it loaded
+    (register loads), recomputed here for a ragged M, three N tiles and two
+    K splits (5 and 5 chunks: one wave with two chunks)."""
+    M, N, K, tm, tn, S = 40, 96, 640, 32, 32, 2
     KS, mb, nb = K // 32, tm // 16, tn // 16
     mtiles, ntiles = (M + tm - 1) // tm, N // tn
     rng = np.random.default_rng(47)
@@ -709,8 +712,8 @@ def test_gemm_walk_probe_reads_each_tiles_blocks():
     W = torch.from_numpy(w_words.view(np.int32)).to(dev())
     nwords = _lib.lib().fc_gemm_walk_probe_words(M, N, tm, tn, S)
     out = torch.zeros(nwords, dtype=torch.int32, device=dev())
-    check(_lib.lib().fc_gemm_walk_probe(A.data_ptr(), W.data_ptr(), M, N, K, tm, tn, S, out.data_ptr(), stream()),
-          "fc_gemm_walk_probe")
+    check(_lib.lib().fc_gemm_walk_probe(A.data_ptr(), W.data_ptr(), M, N, K, tm, tn, S, reg_loads, out.data_ptr(),
+                                        stream()), "fc_gemm_walk_probe")
     torch.cuda.synchronize()
     got = out.cpu().numpy().view(np.uint32).reshape(-1, 4)
     blk_xor = lambda words, i: np.bitwise_xor.reduce(words[i * 256:(i + 1) * 256])  # noqa: E731
@@ -724,17 +727,20 @@ def test_gemm_walk_probe_reads_each_tiles_blocks():
             continue
         mt, rest = t % mtiles, t // mtiles
         sp, nt = rest % S, rest // S
-        k0, k1 = sp * KS // S, (sp + 1) * KS // S
+        C = KS // 2
+        c0, c1 = sp * C // S, (sp + 1) * C // S
         for w in range(4):
             seq = []
-            for ks in range(k0 + w, k1, 4):
-                for b in range(mb + nb):
-                    if b < mb:
-                        seq.append(blk_xor(a_words, min(mt * mb + b, last_blk) * KS + ks))
-                    else:
-                        seq.append(blk_xor(w_words, (nt * nb + b - mb) * KS + ks))
+            for c in range(c0 + w, c1, 4):
+                for b in range(nb + mb):
+                    for h in range(2):
+                        ks = 2 * c + h
+                        if b < nb:
+                            seq.append(blk_xor(w_words, (nt * nb + b) * KS + ks))
+                        else:
+                            seq.append(blk_xor(a_words, min(mt * mb + b - nb, last_blk) * KS + ks))
             x = np.uint32(0)
-            for v in seq[-16:]:
+            for v in (seq if reg_loads else seq[-16:]):
                 x ^= v
             want[g, w] = x
     assert np.array_equal(got, want)
