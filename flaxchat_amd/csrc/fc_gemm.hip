@@ -1708,6 +1708,8 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
     launch_gemv<float>(A, W, Mcap, Mdev, N, K, ee, s);
   } else if (p.big) {
     FC_CHECK_ARG(ee.rms_in == nullptr && ee.xa == nullptr, "the 256 x 256 GEMM has no folded-norm epilogue");
+    FC_CHECK_ARG(p.S == 1 || (p.S == 8 && ee.mode == EPI_PARTIAL && K % 1024 == 0),
+                 "the 256 x 256 GEMM splits K only 8 ways, in multiples of 4 k steps per split");
     launch_big(A, W, Mcap, Mdev, N, K, p.nb, p.S, ee, s);
   } else if (p.ring) {
     if (p.mb == 2) launch_ring<2, 2, 4, 2>(A, W, Mcap, Mdev, N, K, p.S, ee, s);  // 32 x 32, 4 stages
