@@ -202,6 +202,16 @@ __global__ __launch_bounds__(256) void k_gemv(const T* __restrict__ A, const T* 
 // other GEMMs re-read weight tiles across M tiles through L2 and lose more
 // than they gain from it (5.0 -> 5.3 ms).
 #define LM_LD(p) __builtin_nontemporal_load(p)
+// The same for the lm_head on the K-split kernel (one-row decode: cfg2's
+// 100 MB head read five times a round; 0.917-0.918 vs 0.924 ms per round)
+// and on the 256 x 256 kernel's direct loads (the cfg4 verify head:
+// 4.835-4.837 vs 4.840-4.845 ms per round), alternating builds.
+#ifndef FC_KS_LM_NT
+#define FC_KS_LM_NT 1
+#endif
+#ifndef FC_BIG_LM_NT
+#define FC_BIG_LM_NT 1
+#endif
 __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                   0, 0);
@@ -356,7 +366,8 @@ __global__ __launch_bounds__(256) void k_gemm_ks(const bf16_t* __restrict__ A, c
     const int c_ = c_beg + wave + 4 * min((i), nch - 1);                            \
     _Pragma("unroll") for (int j = 0; j < NB; ++j)                                  \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
-        wb[slot][j][ks] = W_LD((const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems)); \
+        wb[slot][j][ks] = EPI == EPI_SOFTCAP && FC_KS_LM_NT ? LM_LD((const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems)) \
+                                                             : W_LD((const v4u*)(wrow[j] + (2 * c_ + ks) * kstep_elems)); \
     _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                               \
       _Pragma("unroll") for (int ks = 0; ks < 2; ++ks)                              \
         ab[slot][mb][ks] = *(const v4u*)(arow[mb] + (2 * c_ + ks) * kstep_elems);   \
@@ -1191,7 +1202,8 @@ __global__ __launch_bounds__(256) void k_gemm_big(const bf16_t* __restrict__ A, 
                                        (__attribute__((address_space(3))) void*)&S.a[4 * wave + u][0], 16, 0, 0); \
     _Pragma("unroll") for (int u = 0; u < NB; ++u)                                                            \
       __builtin_amdgcn_global_load_lds((const void*)(wb[u] + (int64_t)c * 512),                              \
-                                       (__attribute__((address_space(3))) void*)&S.w[NB * wave + u][0], 16, 0, 0); \
+                                       (__attribute__((address_space(3))) void*)&S.w[NB * wave + u][0], 16, 0,   \
+                                       EPI == EPI_SOFTCAP && FC_BIG_LM_NT ? 2 : 0);                          \
   }
 #define BIG_SYNC(NVW)                                                                                         \
   {                                                                                                           \
