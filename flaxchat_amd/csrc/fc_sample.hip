@@ -1040,7 +1040,13 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
 // ---------------------------------------------------------------------------
 #define VP_THR 256
 #define VP_CHUNK (VP_THR * 4)
-#define VP_MAXWG 2048
+// workgroup budget of a vocab pass: rows x chunks (of VP_CHUNK * nv entries)
+// stays within it, nv <= 8. 8192 puts cfg4's 224 verify rows on 32 chunks
+// each instead of 8 (4.796-4.799 vs 4.802-4.807 ms per round, alternating
+// builds); draft rows (32 x 64 chunks) are unchanged.
+#ifndef VP_MAXWG
+#define VP_MAXWG 8192
+#endif
 
 struct VPart {  // one chunk of one logits row
   float zmax; int zarg;  // argmax of z (first index among equals)
