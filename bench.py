@@ -125,6 +125,36 @@ def attention_roofline(sess, n_rep=3):
                 S=res["S"], L=res["L"], nS=nS, nL=nL)
 
 
+def lm_head_gemv(dev, M=32, N=65536, K=1536, n_copies=3, n_rep=4):
+    """The draft lm_head as the engine runs it (fc_gemm at the draft step's row
+    count: the kernel and tiles the engine's plan picks for it, non-temporal
+    weight loads, softcap epilogue into fp32 logits; cfg4: 32 rows on the
+    LDS-shared 32 x 64 tiles), weights cycled over `n_copies` copies so
+    every launch reads them from HBM. GB/s of algorithmic bytes (weights +
+    activations + logits) and us per launch."""
+    import torch
+    from flaxchat_amd import _lib
+    w = torch.ones((n_copies, N, K), dtype=torch.bfloat16, device=dev)
+    a = torch.ones((M, K), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream(dev)
+    run = lambda i: _lib.check(_lib.lib().fc_gemm(a.data_ptr(), w[i % n_copies].data_ptr(), out.data_ptr(),  # noqa: E731
+                                                  M, N, K, _lib.FC_BF16, _lib.EPI_SOFTCAP, s.cuda_stream), "fc_gemm")
+    for i in range(n_copies):
+        run(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(n_rep * n_copies):
+        run(i)
+    e1.record(s)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (n_rep * n_copies)
+    nbytes = N * K * 2 + M * K * 2 + M * N * 4
+    del w, a, out
+    return {"kernel": f"draft lm_head ({M} x {N} x {K}, softcap)", "us": round(us, 2),
+            "achieved": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def copy_ceiling(dev, n_bytes=1 << 30, n_rep=5):
     """Measured streaming ceiling: a device-to-device copy of `n_bytes`
     (the runtime's copy kernel), rated by the bytes it reads plus writes."""
@@ -476,6 +506,8 @@ def main():
         wceil = walk_ceiling(target.device, sess.B * sess.T.G, int(r["per_launch_bytes"]))
         # the GEMMs' operand walks at their tilings (cfg4 shapes)
         gwalks = gemm_walks(target.device) if args.config == "cfg4" else None
+        # the largest GEMV of a draft step, against the same HBM peak
+        gemv = lm_head_gemv(target.device, M=sess.B, K=sess.T.D) if sess.B <= 32 else None
         roof = {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": int(r["per_launch_bytes"] * ATTN_TRAFFIC_RATIO),
@@ -488,7 +520,8 @@ def main():
                 "frac_of_read_ceiling_launch_bytes": round(r["achieved"] / rceil_l, 4),
                 "walk_ceiling": round(wceil, 1), "frac_of_walk_ceiling": round(r["achieved"] / wceil, 4),
                 "l2_read_ceiling_by_workgroups": l2c,
-                "gemm_walks": gwalks}
+                "gemm_walks": gwalks,
+                "draft_lm_head_gemv": gemv}
         print(f"[bench] verify attention {r['achieved']:.0f} GB/s (1 GiB copy: {ceil:.0f} GB/s, "
               f"1 GiB streaming read: {rceil:.0f} GB/s, streaming read of one launch's "
               f"{r['per_launch_bytes'] / 1e6:.0f} MB: {rceil_l:.0f} GB/s; its own load walk: {wceil:.0f} GB/s; "
