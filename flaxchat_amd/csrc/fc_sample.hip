@@ -629,17 +629,36 @@ __device__ __forceinline__ TkRow tk_finish_row(const TkChunk* __restrict__ ch, i
   __shared__ float redv[16];
   __shared__ int redi[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // slot q of thread t: candidate j of chunk cc for t TK_SPT + q = cc TK_MAX + j (index order)
+  // slot q of thread t: candidate j of chunk cc for t TK_SPT + q = cc TK_MAX + j (index order);
+  // a thread's TK_SPT slots are consecutive candidates of one chunk, loaded
+  // as whole 16-byte groups together with the chunk's count (one round trip;
+  // slots past the count are masked afterwards)
+  static_assert(TK_MAX % TK_SPT == 0 && TK_SPT % 4 == 0, "a thread's slots: 16-byte groups of one chunk");
   float zv[TK_SPT], gv[TK_SPT];
   int iv[TK_SPT];
   bool ok[TK_SPT];
+  {
+    const int cc = threadIdx.x * TK_SPT / TK_MAX, j0 = threadIdx.x * TK_SPT - cc * TK_MAX;
+    const TkChunk* c = ch + min(cc, nch - 1);
+    const int n = c->n;
+    float4 z4[TK_SPT / 4], g4[TK_SPT / 4];
+    int4 i4[TK_SPT / 4];
 #pragma unroll
-  for (int q = 0; q < TK_SPT; ++q) {
-    const int sidx = threadIdx.x * TK_SPT + q, cc = sidx / TK_MAX, j = sidx - cc * TK_MAX;
-    ok[q] = cc < nch && j < ch[cc].n;
-    zv[q] = ok[q] ? ch[cc].z[j] : -INFINITY;
-    iv[q] = ok[q] ? ch[cc].idx[j] : 0x7fffffff;
-    gv[q] = ok[q] && draw ? ch[cc].gz[j] : 0.f;
+    for (int u = 0; u < TK_SPT / 4; ++u) {
+      z4[u] = *(const float4*)&c->z[j0 + 4 * u];
+      i4[u] = *(const int4*)&c->idx[j0 + 4 * u];
+      g4[u] = draw ? *(const float4*)&c->gz[j0 + 4 * u] : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int q = 0; q < TK_SPT; ++q) {
+      const float4 zz = z4[q >> 2], gg = g4[q >> 2];
+      const int4 ii = i4[q >> 2];
+      const int w = q & 3;
+      ok[q] = cc < nch && j0 + q < n;
+      zv[q] = ok[q] ? (w == 0 ? zz.x : w == 1 ? zz.y : w == 2 ? zz.z : zz.w) : -INFINITY;
+      iv[q] = ok[q] ? (w == 0 ? ii.x : w == 1 ? ii.y : w == 2 ? ii.z : ii.w) : 0x7fffffff;
+      gv[q] = ok[q] && draw ? (w == 0 ? gg.x : w == 1 ? gg.y : w == 2 ? gg.z : gg.w) : 0.f;
+    }
   }
   const int kk = min(top_k, V);
   uint32_t kz[TK_SPT];
@@ -652,8 +671,11 @@ __device__ __forceinline__ TkRow tk_finish_row(const TkChunk* __restrict__ ch, i
   __shared__ uint32_t cs[TK_NARROW_ROW];
   static_assert(TK_NCH <= 64, "one chunk maximum per lane of a wave");
   if (wave == 0) {
-    const bool has = lane < nch && ch[lane].n > 0;
-    const uint32_t cm[1] = {has ? ch[lane].kmax : 0u};
+    const TkChunk* cl = ch + min(lane, nch - 1);  // count and maximum loaded together
+    const int cn = cl->n;
+    const uint32_t ckmax = cl->kmax;
+    const bool has = lane < nch && cn > 0;
+    const uint32_t cm[1] = {has ? ckmax : 0u};
     const bool co[1] = {has};
     const uint32_t rmax = wave_max_u32(cm[0]);
     uint32_t tlo = 0u;
