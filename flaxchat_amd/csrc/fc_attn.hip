@@ -63,11 +63,12 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
   const int half = hd >> 1;
   const bool act = lane < half;
   const bool vhead = hh >= H + G;
-  // tokens past the device total exit first (a launch covers the chunk's
-  // capacity); then every load that needs neither the token's row nor its
-  // position is issued before any of them is waited for, and the rotary
-  // table and the value-embedding row follow as one second batch
-  if (Mdev != nullptr && m >= *Mdev) return;
+  // every load that needs neither the token's row nor its position (the
+  // device total included: a launch covers the chunk's capacity, and the
+  // loads of a token past the total stay inside it) is issued before any of
+  // them is waited for; tokens past the total then exit, and the rotary table
+  // and the value-embedding row follow as one second batch
+  const int mdev = Mdev != nullptr ? *Mdev : Mcap;
   const int b = tok_row[m], pos = tok_pos[m];
   const float* row = qkv + ((int64_t)m * NH + hh) * hd;
   float x1 = act ? row[lane] : 0.f, x2 = act ? row[lane + half] : 0.f;
@@ -77,6 +78,7 @@ __global__ __launch_bounds__(256) void k_prologue(const float* __restrict__ qkv,
     tok = tokens[m];
     part = lane < 12 ? ld<T>(h, act_idx<T>(m, lane, D)) * ve_gate[(hh - H - G) * 12 + lane] : 0.f;
   }
+  if (m >= mdev) return;
   if ((unsigned)b >= (unsigned)B) return;
   if (!vhead) {
     const int pc = min(max(pos, 0), rope_len - 1);
