@@ -161,6 +161,8 @@ __device__ __forceinline__ uint32_t pick(const u32x4& r, int i) {
 // u in [0, 1) for accept tests.
 __device__ __forceinline__ float u_open(uint32_t bits) { return ((float)(bits >> 9) + 0.5f) * 1.1920928955078125e-7f; }
 __device__ __forceinline__ float u_half(uint32_t bits) { return (float)(bits >> 8) * 5.9604644775390625e-8f; }
+// standard Gumbel noise -log(-log(u)) of one Philox word
+__device__ __forceinline__ float gumbel_of(uint32_t bits) { return -logf(-logf(u_open(bits))); }
 
 // ---------------------------------------------------------------------------
 // Host-side status plumbing

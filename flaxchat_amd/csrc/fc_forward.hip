@@ -360,6 +360,13 @@ static int check_model(const fc_model* m) {
 
 extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chunk* ch, void* work,
                               int64_t work_bytes, void* stream) {
+  int nch = 0;
+  return fc_forward_vp(m, c, ch, work, work_bytes, stream, nullptr, &nch);
+}
+
+int fc_forward_vp(const fc_model* m, const fc_cache* c, const fc_chunk* ch, void* work, int64_t work_bytes,
+                  void* stream, const VocabFuse* vpf, int* nch) {
+  *nch = 0;
   int rc = check_model(m);
   if (rc) return rc;
   FC_CHECK_ARG(c && c->k && c->v && c->hist && c->batch > 0 && c->cap > 0 && c->cap % 32 == 0, "cache");
@@ -540,8 +547,22 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
     e.n_out = ch->n_out;
     e.row_stride = ch->logits_stride;
     e.V = m->vocab;
+    // the draft step's vocab pass folded into its logits GEMM where the
+    // kernel can take it and the caller's partials buffer holds a VPart per
+    // row and column tile
+    const int vt = vpf != nullptr && vpf->vp != nullptr ? fc_gemm_vocab_tiles(Mo, m->vocab_pad, D, dt) : 0;
+    if (vt > 0 && vt <= vpf->max_tiles && (int64_t)Mo * vt <= vpf->vp_cap) {
+      e.vp = vpf->vp;
+      e.vp_ld = vt;
+      e.vp_T = vpf->T;
+      e.vp_draw = vpf->draw;
+      e.vp_slot = vpf->slot;
+      e.vp_seed = vpf->seed;
+      e.vp_round = vpf->round;
+    }
     rc = fc_launch_gemm(w.h, m->lm_head, Mo, nullptr, Mo, m->vocab_pad, D, dt, e, w.gw, s, nullptr);
     if (rc) return rc;
+    if (e.vp != nullptr) *nch = vt;
   }
   return FC_OK;
 }

@@ -559,9 +559,129 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
   }
 }
 
+// Vocab-pass partials of the logits tile (EPI_SOFTCAP with e.vp): the same
+// terms as the separate pass (k_vpart) over the tile's columns instead of a
+// 1024-entry chunk, so the draft step needs no second pass over its logits.
+// Per 32 rows the capped values are staged in LDS; then 8 consecutive lanes
+// own a row, NT / 8 columns each (whole Philox groups of 4), and reduce with
+// shuffles; lane 0 of the 8 writes the row's VPart.
+// The capped logits are stored here too, from the same values the partials
+// are computed from (acc is overwritten with them).
+template <int MB, int NBW>
+__device__ __forceinline__ void vocab_tile_parts(const Epi& e, f32x4 (&acc)[MB][NBW], int m0, int n0, int nt,
+                                                 int M) {
+  constexpr int NT = 64 * NBW, PER = NT / 8, LD = NT + 4;
+  static_assert(MB % 2 == 0, "32-row passes");
+  __shared__ __align__(16) float T[32 * LD];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int row = threadIdx.x >> 3, q = threadIdx.x & 7;
+  const int c0 = n0 + q * PER;  // this thread's first column
+  const float Tt = e.vp_T;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float z = softcap15_fast(acc[mb][j][i]);
+        acc[mb][j][i] = z;
+        const int m = m0 + 16 * mb + 4 * g + i, n = n0 + 16 * (wave * NBW + j) + r;
+        if (m < M && n < e.V) {
+          const int b = m / e.n_out, rr = m - b * e.n_out;
+          ((float*)e.out)[(int64_t)b * e.row_stride + (int64_t)rr * e.V + n] = z;
+        }
+      }
+#pragma unroll
+  for (int p = 0; p < MB / 2; ++p) {
+    if (p > 0) __syncthreads();  // the previous pass's readers are done with T
+#pragma unroll
+    for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) T[(16 * mh + 4 * g + i) * LD + 16 * (wave * NBW + j) + r] = acc[2 * p + mh][j][i];
+    __syncthreads();
+    const int m = m0 + 32 * p + row;
+    float v[PER];
+#pragma unroll
+    for (int w = 0; w < PER; w += 4) {
+      const float4 t4 = *reinterpret_cast<const float4*>(&T[row * LD + q * PER + w]);
+      v[w] = t4.x;
+      v[w + 1] = t4.y;
+      v[w + 2] = t4.z;
+      v[w + 3] = t4.w;
+    }
+    float bz = -INFINITY;
+    int bzi = 0x7fffffff;
+#pragma unroll
+    for (int w = 0; w < PER; ++w)
+      if (c0 + w < e.V) argmax_merge(bz, bzi, v[w], c0 + w);
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) argmax_merge(bz, bzi, __shfl_xor(bz, o, WAVE), __shfl_xor(bzi, o, WAVE));
+    VPart pt;
+    pt.zmax = bz;
+    pt.zarg = bzi;
+    pt.m = 0.f;
+    pt.s = 1.f;
+    pt.a = -INFINITY;
+    pt.ai = 0x7fffffff;
+    pt.g = -INFINITY;
+    pt.gi = 0x7fffffff;
+    if (Tt > 0.f) {
+      const float mx = bz / Tt;
+#pragma unroll
+      for (int w = 0; w < PER; ++w) v[w] = v[w] / Tt;
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < PER; ++w)
+        if (c0 + w < e.V) sum += expf(v[w] - mx);
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, WAVE);
+      pt.m = mx;
+      pt.s = sum;
+      if (e.vp_draw) {
+        const int rnd = m < M ? e.vp_round[m] : 0;
+        float ba = -INFINITY, bg = -INFINITY;
+        int bai = 0x7fffffff, bgi = 0x7fffffff;
+#pragma unroll
+        for (int w0 = 0; w0 < PER; w0 += 4) {
+          if (c0 + w0 >= e.V) break;
+          const u32x4 rr = philox4x32_10(u32x4{(uint32_t)((c0 + w0) >> 2), (uint32_t)m, (uint32_t)rnd,
+                                               (uint32_t)e.vp_slot},
+                                         (uint32_t)e.vp_seed, (uint32_t)(e.vp_seed >> 32));
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int i = c0 + w0 + w;
+            if (i >= e.V) break;
+            const float G = gumbel_of(pick(rr, w));
+            argmax_merge(ba, bai, (v[w0 + w] - mx) + G, i);
+            argmax_merge(bg, bgi, G, i);
+          }
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+          argmax_merge(ba, bai, __shfl_xor(ba, o, WAVE), __shfl_xor(bai, o, WAVE));
+          argmax_merge(bg, bgi, __shfl_xor(bg, o, WAVE), __shfl_xor(bgi, o, WAVE));
+        }
+        pt.a = ba;
+        pt.ai = bai;
+        pt.g = bg;
+        pt.gi = bgi;
+      }
+    }
+    if (q == 0 && m < M) {
+      float4* dst = reinterpret_cast<float4*>(e.vp + (int64_t)m * e.vp_ld + nt);
+      dst[0] = make_float4(pt.zmax, __int_as_float(pt.zarg), pt.m, pt.s);
+      dst[1] = make_float4(pt.a, __int_as_float(pt.ai), pt.g, __int_as_float(pt.gi));
+    }
+  }
+}
+
 // Epilogue of the column-split kernels (k_gemm_la, k_gemm_dma): acc[mb][j]
-// holds rows 16 mb + 4 g + i, column 16 (wave NBW + j) + r of the tile.
-template <int MB, int NBW, int EPI>
+// holds rows 16 mb + 4 g + i, column 16 (wave NBW + j) + r of the tile. VP:
+// the kernel can write the vocab-pass partials (k_gemm_la).
+template <int MB, int NBW, int EPI, bool VP = false>
 __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[MB][NBW], const RmsPre& rpre,
                                               QkvPre (&qpre)[(MB + 1) / 2], int m0, int n0, int nt, int s, int M,
                                               int K) {
@@ -606,6 +726,17 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[M
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) rsc[mb][i] = rowinv[16 * mb + 4 * g + i];
+      }
+    }
+    if constexpr (VP && EPI == EPI_SOFTCAP && MB % 2 == 0) {
+      if (e.vp != nullptr) {
+        f32x4 z[MB][NBW];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int j = 0; j < NBW; ++j) z[mb][j] = acc[mb][j];
+        vocab_tile_parts<MB, NBW>(e, z, m0, n0, nt, M);
+        return;
       }
     }
     Epi ee = e;
@@ -744,7 +875,7 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #undef LA_STAGE_A
   }
 
-  tile_epilogue<MB, NBW, EPI>(e, acc, rpre, qpre, m0, n0, nt, s, M, K);
+  tile_epilogue<MB, NBW, EPI, true>(e, acc, rpre, qpre, m0, n0, nt, s, M, K);
 }
 
 // bf16 MFMA GEMM for verify-size row counts with both operands staged in an
@@ -1708,6 +1839,9 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
     p = plan_fold_add(Mtyp, N);
   }
   if (p.S > 1 && (int64_t)p.S * Mcap * N * 4 > gw.part_bytes) p.S = 1;
+  FC_CHECK_ARG(e.vp == nullptr || (e.mode == EPI_SOFTCAP && p.la && p.S == 1 && p.mb % 2 == 0 &&
+                                   e.vp_ld == N / (64 * (p.mb == 8 || p.nb != 1 ? 2 : 1))),
+               "vocab-pass partials: an unsplit EPI_SOFTCAP GEMM on the LDS-shared kernel, vp_ld = its column tiles");
   Epi ee = e;
   if (p.S > 1) {
     ee.mode = EPI_PARTIAL;
@@ -1742,6 +1876,13 @@ int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int 
   }
   FC_LAUNCH_CHECK();
   return FC_OK;
+}
+
+int fc_gemm_vocab_tiles(int M, int N, int K, int dtype) {
+  if (M <= 0 || N <= 0 || dtype != FC_BF16 || K % 64 != 0 || N % 32 != 0) return 0;
+  const GemmPlan p = plan_gemm(M, N, K, dtype, false);
+  if (!p.la || p.S != 1 || p.mb % 2 != 0) return 0;
+  return N / (64 * (p.mb == 8 || p.nb != 1 ? 2 : 1));  // launch_la<8, 2>, <2, 1> or <2, 2>
 }
 
 extern "C" int32_t fc_gemm(const void* A, const void* W, void* out, int32_t M, int32_t N, int32_t K, int32_t dtype,

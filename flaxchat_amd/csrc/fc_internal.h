@@ -20,6 +20,15 @@ struct QkvEpi {
   uint16_t *kc, *vc, *q;  // layer's K / V cache, q output
 };
 
+// Vocab-pass partials of one logits row over one range of its entries
+// (a chunk of the separate pass, or a column tile of the lm_head GEMM)
+struct VPart {
+  float zmax; int zarg;  // argmax of z (first index among equals)
+  float m, s;            // max of x = z / T and sum of exp(x - m)
+  float a; int ai;       // max of x - m + G, and its index
+  float g; int gi;       // max of G, and its index
+};
+
 struct Epi {
   int mode;
   int out_dtype;
@@ -34,6 +43,16 @@ struct Epi {
   int n_out;
   int64_t row_stride;
   int V;
+  // EPI_SOFTCAP given `vp` (the LDS-shared kernel only): also the vocab-pass
+  // partials of output row m over the tile's columns, vp[m * vp_ld + column
+  // tile], at temperature vp_T (> 0: max / exp-sum of z / T, and with
+  // vp_draw the Gumbel-max terms of Philox counter (column / 4, m,
+  // vp_round[m], vp_slot) under key vp_seed; else the argmax alone)
+  VPart* vp;
+  int vp_ld, vp_draw, vp_slot;
+  float vp_T;
+  uint64_t vp_seed;
+  const int* vp_round;
   // EPI_PARTIAL: split `split` writes part[(split * part_rows + m) * ldo + n]
   float* part;
   int part_rows, split;
@@ -70,6 +89,24 @@ bool fc_gemm_fuses_qkv(int Mtyp, int N, int K, int dtype, int head_dim);
 int fc_launch_gemm(const void* A, const void* W, int Mcap, const int* Mdev, int Mtyp, int N, int K, int dtype,
                    const Epi& e, const GemmWork& gw,
                    hipStream_t s, int* splits);
+// column tiles per row of an unsplit EPI_SOFTCAP GEMM of this shape when its
+// kernel can write the vocab-pass partials (Epi::vp), else 0
+int fc_gemm_vocab_tiles(int M, int N, int K, int dtype);
+// fc_forward whose logits GEMM also writes the vocab-pass partials where its
+// kernel can (see Epi::vp; `vp` may be NULL): *nch = partials per logits row
+// then, else 0 (the caller runs the separate pass). `vp_cap` = VParts at vp;
+// a GEMM with more than `max_tiles` column tiles is left to the separate pass.
+struct VocabFuse {
+  VPart* vp;
+  int64_t vp_cap;
+  int max_tiles;
+  float T;
+  int draw, slot;
+  uint64_t seed;
+  const int* round;
+};
+int fc_forward_vp(const fc_model* m, const fc_cache* c, const fc_chunk* ch, void* work, int64_t work_bytes,
+                  void* stream, const VocabFuse* vp, int* nch);
 
 struct AttnGrid {
   int nqblk, nsplit, split_keys;

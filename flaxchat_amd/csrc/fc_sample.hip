@@ -185,8 +185,6 @@ __device__ __forceinline__ float prob_at(const float* z, const fc_rowstat& rs, f
   return kept(z[i], i, mono(rs.tau), rs.tie_idx) ? expf(z[i] / T - rs.mx) / rs.sum : 0.f;
 }
 
-__device__ __forceinline__ float gumbel_of(uint32_t bits) { return -logf(-logf(u_open(bits))); }
-
 // Gumbel-max draw over V entries; mode 0: p, mode 1: residual max(0, p - q)
 // renormalised (falls back to p when its mass is zero).
 __device__ int block_draw(const float* __restrict__ zp, const fc_rowstat& sp, const float* __restrict__ zq,
@@ -1070,12 +1068,6 @@ __global__ __launch_bounds__(NTHR) void k_accept(SpecDev s) {
 #define VP_MAXWG 8192
 #endif
 
-struct VPart {  // one chunk of one logits row
-  float zmax; int zarg;  // argmax of z (first index among equals)
-  float m, s;            // max of x = z / T and sum of exp(x - m)
-  float a; int ai;       // max of x - m + G, and its index
-  float g; int gi;       // max of G, and its index
-};
 struct DPart {  // one chunk of a draw from finished row statistics
   float sc; int si;      // max of log(max(p, 1e-10)) + G
   float A; int Ai;       // residual: max of log r + G over r = max(p - q, 0) > 0
@@ -1291,6 +1283,81 @@ __global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, const
   }
 }
 
+// The merge of wave_merge_row by a whole workgroup, for rows of many
+// partials (the logits GEMM's column tiles: up to VP_THR * MAXP): every
+// thread loads its MAXP partials at once, then three block reductions in a
+// fixed order.
+template <int MAXP>
+__device__ RowMerge block_merge_row(const VPart* __restrict__ p, int nch, bool samp, bool draw) {
+  __shared__ float redv[2 * (VP_THR / 64)];
+  __shared__ int redi[2 * (VP_THR / 64)];
+  float4 lo[MAXP], hi[MAXP];
+#pragma unroll
+  for (int u = 0; u < MAXP; ++u) {
+    const int c = threadIdx.x + u * VP_THR;
+    if (c < nch) {
+      const float4* src = reinterpret_cast<const float4*>(p + c);
+      lo[u] = src[0];
+      hi[u] = src[1];
+    } else {
+      lo[u] = make_float4(-INFINITY, __int_as_float(0x7fffffff), -INFINITY, 0.f);
+      hi[u] = make_float4(-INFINITY, __int_as_float(0x7fffffff), -INFINITY, __int_as_float(0x7fffffff));
+    }
+  }
+  float M = -INFINITY, zm = -INFINITY;
+  int zi = 0x7fffffff;
+#pragma unroll
+  for (int u = 0; u < MAXP; ++u) {
+    M = fmaxf(M, lo[u].z);
+    argmax_merge(zm, zi, lo[u].x, __float_as_int(lo[u].y));
+  }
+  M = block_max(M, redv);
+  block_argmax(zm, zi, redv, redi);
+  RowMerge rm;
+  rm.argmax = zi;
+  rm.M = 0.f;
+  rm.S = 1.f;
+  rm.tok = zi;
+  if (!samp) return rm;
+  float S = 0.f;
+#pragma unroll
+  for (int u = 0; u < MAXP; ++u)
+    if (lo[u].z != -INFINITY) S += lo[u].w * expf(lo[u].z - M);
+  S = block_sum(S, redv);
+  rm.M = M;
+  rm.S = S;
+  if (draw) {
+    const float lS = logf(S), lf = log_floor();
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < MAXP; ++u) {
+      argmax_merge(bv, bi, hi[u].x - ((M - lo[u].z) + lS), __float_as_int(hi[u].y));
+      argmax_merge(bv, bi, lf + hi[u].z, __float_as_int(hi[u].w));
+    }
+    block_argmax(bv, bi, redv, redi);
+    rm.tok = bi;
+  }
+  return rm;
+}
+
+// Draft step i when the logits GEMM wrote the partials (one per column tile):
+// one workgroup per row.
+#define VP_WIDE_MAXP 4
+#ifndef FC_DRAFT_VP_FUSE
+#define FC_DRAFT_VP_FUSE 1
+#endif
+__global__ __launch_bounds__(VP_THR) void k_draft_finish_wide(SpecDev s, int i, const VPart* __restrict__ part,
+                                                              int nch) {
+  const int b = blockIdx.x;
+  const bool samp = s.T > 0.f;
+  const RowMerge rm = block_merge_row<VP_WIDE_MAXP>(part + (int64_t)b * nch, nch, samp, samp);
+  if (threadIdx.x == 0) {
+    s.q_stats[b * s.k + i] = make_rowstat(rm, s.V);
+    place_draft(s, b, i, rm.tok);
+  }
+}
+
 // Verify rows without top-k: merge the k+1 rows' partials into p_stats,
 // decide, and record the draw requests for k_draw_part.
 __global__ __launch_bounds__(VP_THR) void k_accept_decide(SpecDev s, const VPart* __restrict__ part, int nch,
@@ -1462,12 +1529,17 @@ struct PartLayout {
   DPart* dp;
   TkChunk* tk;  // top-k candidates of up to batch x (k + 1) rows
   int64_t bytes;
+  int64_t vp_cap;  // VParts at vp
 };
 static PartLayout part_layout(void* base, int B, int K, int V) {
   const int64_t nch1 = vp_nch(V, 1);
   PartLayout L;
+  // VParts: the k + 1 verify rows' chunks, or one per 64-column tile of a
+  // draft step's logits row (vocab padded to a multiple of 64) when its
+  // logits GEMM writes them
+  L.vp_cap = (int64_t)B * std::max((int64_t)(K + 1) * nch1, (int64_t)(V + 63) / 64);
   const int64_t o_vp = fc_align((int64_t)B * sizeof(Decision));
-  const int64_t o_dp = o_vp + fc_align((int64_t)B * (K + 1) * nch1 * sizeof(VPart));
+  const int64_t o_dp = o_vp + fc_align(L.vp_cap * (int64_t)sizeof(VPart));
   const int64_t o_tk = o_dp + fc_align((int64_t)B * 2 * nch1 * sizeof(DPart));
   L.bytes = o_tk + fc_align((int64_t)B * (K + 1) * tk_nch(V) * sizeof(TkChunk));
   char* p = (char*)base;
@@ -1633,9 +1705,26 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
       ch.start = st->start_d + (int64_t)i * B;
     }
     ch.logits = st->q_logits + (int64_t)i * V;
-    rc = fc_forward(draft, dcache, &ch, work, work_bytes, stream);
+    // without top-k the draft's logits GEMM also writes the vocab-pass
+    // partials where its kernel can (one per 64 / 128-column tile; Philox
+    // counter row = batch row b, as in the separate pass)
+    VocabFuse vf{};
+    if (fast && FC_DRAFT_VP_FUSE) {
+      vf.vp = L.vp;
+      vf.vp_cap = L.vp_cap;
+      vf.max_tiles = VP_THR * VP_WIDE_MAXP;
+      vf.T = st->temperature;
+      vf.draw = st->temperature > 0.f;
+      vf.slot = i;
+      vf.seed = st->seed;
+      vf.round = st->round;
+    }
+    int fused = 0;
+    rc = fc_forward_vp(draft, dcache, &ch, work, work_bytes, stream, fast ? &vf : nullptr, &fused);
     if (rc) return rc;
-    if (fast) {
+    if (fast && fused > 0) {
+      hipLaunchKernelGGL(k_draft_finish_wide, dim3(B), dim3(VP_THR), 0, s, d, i, L.vp, fused);
+    } else if (fast) {
       int nch = 0;
       rc = launch_vpart(st->q_logits + (int64_t)i * V, (int64_t)K * V, B, V, st->temperature, st->temperature > 0.f,
                         st->seed, st->round, i, L.vp, &nch, s);
