@@ -559,6 +559,38 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
   }
 }
 
+// The draw's Gumbel noise for this thread's epilogue columns (row m0 + t / 8,
+// NT / 8 columns from n0 + (t % 8) NT / 8), which depends only on the Philox
+// counter: where the tile has a single 32-row pass (MB = 2) k_gemm_la computes
+// it before its K loop, while the first chunks load, instead of in the tail.
+template <int MB, int NBW>
+struct VpNoise {
+  float g[MB == 2 ? 8 * NBW : 1];
+  bool ok;
+};
+template <int MB, int NBW>
+__device__ __forceinline__ bool vp_noise_wanted(const Epi& e) {
+  return MB == 2 && e.vp != nullptr && e.vp_draw && e.vp_T > 0.f;
+}
+template <int MB, int NBW>
+__device__ __forceinline__ void vp_noise(const Epi& e, int m0, int n0, int rnd, VpNoise<MB, NBW>& nz) {
+  nz.ok = false;
+  if constexpr (MB == 2) {
+    if (!vp_noise_wanted<MB, NBW>(e)) return;
+    constexpr int PER = 8 * NBW;
+    const int m = m0 + (threadIdx.x >> 3), c0 = n0 + (threadIdx.x & 7) * PER;
+#pragma unroll
+    for (int w0 = 0; w0 < PER; w0 += 4) {
+      const u32x4 rr = philox4x32_10(u32x4{(uint32_t)((c0 + w0) >> 2), (uint32_t)m, (uint32_t)rnd,
+                                           (uint32_t)e.vp_slot},
+                                     (uint32_t)e.vp_seed, (uint32_t)(e.vp_seed >> 32));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) nz.g[w0 + w] = gumbel_of(pick(rr, w));
+    }
+    nz.ok = true;
+  }
+}
+
 // Vocab-pass partials of the logits tile (EPI_SOFTCAP with e.vp): the same
 // terms as the separate pass (k_vpart) over the tile's columns instead of a
 // 1024-entry chunk, so the draft step needs no second pass over its logits.
@@ -569,7 +601,7 @@ __device__ __forceinline__ void qkv_finish(const QkvEpi& Q, const float* x, int 
 // are computed from (acc is overwritten with them).
 template <int MB, int NBW>
 __device__ __forceinline__ void vocab_tile_parts(const Epi& e, f32x4 (&acc)[MB][NBW], int m0, int n0, int nt,
-                                                 int M) {
+                                                 int M, const VpNoise<MB, NBW>* nz) {
   constexpr int NT = 64 * NBW, PER = NT / 8, LD = NT + 4;
   static_assert(MB % 2 == 0, "32-row passes");
   __shared__ __align__(16) float T[32 * LD];
@@ -644,19 +676,34 @@ __device__ __forceinline__ void vocab_tile_parts(const Epi& e, f32x4 (&acc)[MB][
         const int rnd = m < M ? e.vp_round[m] : 0;
         float ba = -INFINITY, bg = -INFINITY;
         int bai = 0x7fffffff, bgi = 0x7fffffff;
+        bool pre = false;
+        if constexpr (MB == 2) {
+          if (nz != nullptr && nz->ok) {  // the noise computed before the K loop
+            pre = true;
 #pragma unroll
-        for (int w0 = 0; w0 < PER; w0 += 4) {
-          if (c0 + w0 >= e.V) break;
-          const u32x4 rr = philox4x32_10(u32x4{(uint32_t)((c0 + w0) >> 2), (uint32_t)m, (uint32_t)rnd,
-                                               (uint32_t)e.vp_slot},
-                                         (uint32_t)e.vp_seed, (uint32_t)(e.vp_seed >> 32));
+            for (int w = 0; w < PER; ++w) {
+              const int i = c0 + w;
+              if (i >= e.V) break;
+              argmax_merge(ba, bai, (v[w] - mx) + nz->g[w], i);
+              argmax_merge(bg, bgi, nz->g[w], i);
+            }
+          }
+        }
+        if (!pre) {
 #pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const int i = c0 + w0 + w;
-            if (i >= e.V) break;
-            const float G = gumbel_of(pick(rr, w));
-            argmax_merge(ba, bai, (v[w0 + w] - mx) + G, i);
-            argmax_merge(bg, bgi, G, i);
+          for (int w0 = 0; w0 < PER; w0 += 4) {
+            if (c0 + w0 >= e.V) break;
+            const u32x4 rr = philox4x32_10(u32x4{(uint32_t)((c0 + w0) >> 2), (uint32_t)m, (uint32_t)rnd,
+                                                 (uint32_t)e.vp_slot},
+                                           (uint32_t)e.vp_seed, (uint32_t)(e.vp_seed >> 32));
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const int i = c0 + w0 + w;
+              if (i >= e.V) break;
+              const float G = gumbel_of(pick(rr, w));
+              argmax_merge(ba, bai, (v[w0 + w] - mx) + G, i);
+              argmax_merge(bg, bgi, G, i);
+            }
           }
         }
 #pragma unroll
@@ -684,7 +731,7 @@ __device__ __forceinline__ void vocab_tile_parts(const Epi& e, f32x4 (&acc)[MB][
 template <int MB, int NBW, int EPI, bool VP = false>
 __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[MB][NBW], const RmsPre& rpre,
                                               QkvPre (&qpre)[(MB + 1) / 2], int m0, int n0, int nt, int s, int M,
-                                              int K) {
+                                              int K, const VpNoise<MB, NBW>* nz = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   if constexpr (EPI == EPI_QKV) {
@@ -735,7 +782,7 @@ __device__ __forceinline__ void tile_epilogue(const Epi& e, const f32x4 (&acc)[M
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int j = 0; j < NBW; ++j) z[mb][j] = acc[mb][j];
-        vocab_tile_parts<MB, NBW>(e, z, m0, n0, nt, M);
+        vocab_tile_parts<MB, NBW>(e, z, m0, n0, nt, M, nz);
         return;
       }
     }
@@ -819,6 +866,15 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #pragma unroll
     for (int p = 0; p < MB / 2; ++p) qkv_pre_row(e.qkv, m0 + 32 * p + (threadIdx.x >> 3), M, nt, qpre[p]);
   }
+  // EPI_SOFTCAP draw noise: the row's round counter loads ahead of the
+  // operands, so waiting for it does not wait for them
+  VpNoise<MB, NBW> nz;
+  nz.ok = false;
+  int vp_rnd = 0;
+  if constexpr (EPI == EPI_SOFTCAP && MB == 2) {
+    const int mrow = m0 + (threadIdx.x >> 3);
+    if (vp_noise_wanted<MB, NBW>(e) && mrow < M) vp_rnd = e.vp_round[mrow];
+  }
   f32x4 acc[MB][NBW];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -844,6 +900,7 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
   }
 #pragma unroll
     for (int p = 0; p < NS; ++p) LA_LOAD(p, p);
+    if constexpr (EPI == EPI_SOFTCAP && MB == 2) vp_noise<MB, NBW>(e, m0, n0, vp_rnd, nz);
     LA_STAGE_A(0, 0);
     __syncthreads();
     for (int i0 = 0; i0 < n; i0 += NS) {
@@ -875,7 +932,7 @@ __global__ __launch_bounds__(256) void k_gemm_la(const bf16_t* __restrict__ A, c
 #undef LA_STAGE_A
   }
 
-  tile_epilogue<MB, NBW, EPI, true>(e, acc, rpre, qpre, m0, n0, nt, s, M, K);
+  tile_epilogue<MB, NBW, EPI, true>(e, acc, rpre, qpre, m0, n0, nt, s, M, K, &nz);
 }
 
 // bf16 MFMA GEMM for verify-size row counts with both operands staged in an
