@@ -15,6 +15,7 @@
 //   q, y, hid   attention query / output and the ReLU^2 hidden (model dtype)
 #include "fc_common.h"
 #include "fc_internal.h"
+#include "fc_vocab.h"
 
 #define EMBED_MAXW 1024
 
@@ -57,9 +58,17 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
                                                const int* __restrict__ start, int max_per_row, int Mcap, int D,
                                                int cap, float* __restrict__ hist, float* __restrict__ x,
                                                float* __restrict__ x0, int* __restrict__ tok_row,
-                                               int* __restrict__ tok_pos, int full_smear, bf16_t* __restrict__ h) {
+                                               int* __restrict__ tok_pos, int full_smear, bf16_t* __restrict__ h,
+                                               DraftMerge dm) {
   __shared__ float sg[EMBED_MAXW], sinv[EMBED_MAXW];
   const int b = blockIdx.x;
+  // NORM with dm.part: first finish the previous draft step for this row; its
+  // draft is the row's one token here (written to tokens[] for the later
+  // kernels by thread 0, so this kernel reads it from the merge, not memory)
+  int merged = -1;
+  if constexpr (NORM) {
+    if (dm.part != nullptr) merged = draft_merge_row(dm, b);
+  }
   const RowSpan sp = row_span(row_off, b, max_per_row, Mcap);
   const int base = sp.base, n = sp.n, s0 = start[b];
   if (n <= 0 || s0 < 0) {
@@ -77,7 +86,7 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
   }
   // per token: 1 / rms of the embedding row and the smear gate
   for (int j = wave; j < n; j += 4) {
-    const T* e = wte + (int64_t)tokens[base + j] * D;
+    const T* e = wte + (int64_t)(merged >= 0 ? merged : tokens[base + j]) * D;
     float ss = 0.f;
     for (int d = lane * 8; d < D; d += 64 * 8) {
       float v[8];
@@ -110,7 +119,7 @@ __global__ __launch_bounds__(256) void k_embed(const T* __restrict__ wte, const 
       float ev[EMBED_NORM_MAX][8];
 #pragma unroll
       for (int j = 0; j < EMBED_NORM_MAX; ++j)
-        if (j < n) ld8(wte + (int64_t)tokens[base + j] * D + c0, ev[j]);
+        if (j < n) ld8(wte + (int64_t)(merged >= 0 ? merged : tokens[base + j]) * D + c0, ev[j]);
 #pragma unroll
       for (int j = 0; j < EMBED_NORM_MAX; ++j) {
         if (j < n) {
@@ -364,8 +373,15 @@ extern "C" int32_t fc_forward(const fc_model* m, const fc_cache* c, const fc_chu
   return fc_forward_vp(m, c, ch, work, work_bytes, stream, nullptr, &nch);
 }
 
+// bf16 chunks of at most EMBED_NORM_MAX tokens per row (n_embd <= 2048): the
+// embedding kernel also writes the first layer's RMSNorm output, and can
+// finish the previous draft step (DraftMerge)
+bool fc_embed_merges(const fc_model* m, const fc_chunk* ch) {
+  return m->dtype == FC_BF16 && ch->max_per_row <= EMBED_NORM_MAX && m->n_embd <= 2048 && m->n_embd % 8 == 0;
+}
+
 int fc_forward_vp(const fc_model* m, const fc_cache* c, const fc_chunk* ch, void* work, int64_t work_bytes,
-                  void* stream, const VocabFuse* vpf, int* nch) {
+                  void* stream, const VocabFuse* vpf, int* nch, const DraftMerge* dm) {
   *nch = 0;
   int rc = check_model(m);
   if (rc) return rc;
@@ -398,22 +414,27 @@ int fc_forward_vp(const fc_model* m, const fc_cache* c, const fc_chunk* ch, void
 
   // bf16 chunks of few tokens per row: the embedding kernel also writes the
   // first layer's RMSNorm output (h), and that layer's RMSNorm launch is skipped
-  const bool embed_norm = dt == FC_BF16 && ch->max_per_row <= EMBED_NORM_MAX && D <= 2048 && D % 8 == 0;
+  const bool embed_norm = fc_embed_merges(m, ch);
+  // the previous draft step's merge, run by this chunk's embedding kernel
+  FC_CHECK_ARG(dm == nullptr || (embed_norm && ch->max_per_row == 1 && dm->part && dm->nch > 0 &&
+                                 dm->nch <= FC_VOCAB_THR * VP_WIDE_MAXP && dm->B == B),
+               "draft merge: a one-token-per-row bf16 draft chunk, at most 1024 partials per row");
+  const DraftMerge dmv = dm != nullptr ? *dm : DraftMerge{};
   if (embed_norm)
     hipLaunchKernelGGL((k_embed<bf16_t, true>), dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
                        ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
-                       full_smear, (bf16_t*)w.h);
+                       full_smear, (bf16_t*)w.h, dmv);
   else if (dt == FC_BF16)
     hipLaunchKernelGGL((k_embed<bf16_t, false>), dim3(B), dim3(256), 0, s, (const bf16_t*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
                        ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
-                       full_smear, nullptr);
+                       full_smear, nullptr, DraftMerge{});
   else
     hipLaunchKernelGGL((k_embed<float, false>), dim3(B), dim3(256), 0, s, (const float*)m->wte, m->smear_gate,
                        m->smear_lambda, m->layers[0].resid_lambda, m->layers[0].x0_lambda, ch->tokens, ch->row_off,
                        ch->start, ch->max_per_row, Mcap, D, c->cap, c->hist, w.x, w.x0, w.tok_row, w.tok_pos,
-                       full_smear, nullptr);
+                       full_smear, nullptr, DraftMerge{});
   FC_LAUNCH_CHECK();
 
   Pending pend{};

@@ -105,8 +105,21 @@ struct VocabFuse {
   uint64_t seed;
   const int* round;
 };
+// The previous draft step's finish (fc_vocab.h draft_merge_row), which the
+// embedding kernel of a one-token-per-row bf16 draft chunk can run itself
+// (fc_embed_merges): row b's token is the merged draft of step `step`.
+struct DraftMerge {
+  const VPart* part;
+  int nch;
+  fc_rowstat* q_stats;
+  int *drafts, *tok_v, *tok_ds;
+  const int *off_v, *off_ds;
+  int B, k, V, step;
+  float T;
+};
+bool fc_embed_merges(const fc_model* m, const fc_chunk* ch);
 int fc_forward_vp(const fc_model* m, const fc_cache* c, const fc_chunk* ch, void* work, int64_t work_bytes,
-                  void* stream, const VocabFuse* vp, int* nch);
+                  void* stream, const VocabFuse* vp, int* nch, const DraftMerge* dm = nullptr);
 
 struct AttnGrid {
   int nqblk, nsplit, split_keys;

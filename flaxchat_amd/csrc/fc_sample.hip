@@ -11,6 +11,7 @@
 // as jax.random.categorical on the reference's log(max(p, 1e-10)) input.
 #include "fc_common.h"
 #include "fc_internal.h"
+#include "fc_vocab.h"
 #include <mutex>
 
 #define SLOT_ACCEPT 16
@@ -1076,7 +1077,6 @@ struct DPart {  // one chunk of a draw from finished row statistics
 };
 static_assert(sizeof(VPart) == 32 && sizeof(DPart) == 32, "partial layout");
 
-__device__ __forceinline__ float log_floor() { return logf(1e-10f); }
 
 // Four entries e..e+3 of row z (-inf beyond V).
 __device__ __forceinline__ void load4(const float* __restrict__ z, int e, int V, bool vec, float* v) {
@@ -1223,7 +1223,6 @@ static int launch_vpart(const float* z0, int64_t row_stride, int rows, int V, fl
 
 // One wave merges the nch partials of a row: statistics and (with `draw`)
 // the winner of the row's draw.
-struct RowMerge { float M, S; int argmax, tok; };
 __device__ RowMerge wave_merge_row(const VPart* __restrict__ p, int nch, bool samp, bool draw) {
   const int lane = threadIdx.x & 63;
   float M = -INFINITY, zm = -INFINITY;
@@ -1259,16 +1258,6 @@ __device__ RowMerge wave_merge_row(const VPart* __restrict__ p, int nch, bool sa
   return rm;
 }
 
-__device__ __forceinline__ fc_rowstat make_rowstat(const RowMerge& rm, int V) {
-  fc_rowstat rs{};
-  rs.mx = rm.M;
-  rs.sum = rm.S;
-  rs.tau = -INFINITY;
-  rs.tie_idx = V;
-  rs.argmax = rm.argmax;
-  return rs;
-}
-
 // Draft step i without top-k: merge of the step's partials (one wave per row),
 // proposal d_{i+1} written where the next chunks read it.
 __global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, const VPart* __restrict__ part,
@@ -1283,79 +1272,33 @@ __global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, const
   }
 }
 
-// The merge of wave_merge_row by a whole workgroup, for rows of many
-// partials (the logits GEMM's column tiles: up to VP_THR * MAXP): every
-// thread loads its MAXP partials at once, then three block reductions in a
-// fixed order.
-template <int MAXP>
-__device__ RowMerge block_merge_row(const VPart* __restrict__ p, int nch, bool samp, bool draw) {
-  __shared__ float redv[2 * (VP_THR / 64)];
-  __shared__ int redi[2 * (VP_THR / 64)];
-  float4 lo[MAXP], hi[MAXP];
-#pragma unroll
-  for (int u = 0; u < MAXP; ++u) {
-    const int c = threadIdx.x + u * VP_THR;
-    if (c < nch) {
-      const float4* src = reinterpret_cast<const float4*>(p + c);
-      lo[u] = src[0];
-      hi[u] = src[1];
-    } else {
-      lo[u] = make_float4(-INFINITY, __int_as_float(0x7fffffff), -INFINITY, 0.f);
-      hi[u] = make_float4(-INFINITY, __int_as_float(0x7fffffff), -INFINITY, __int_as_float(0x7fffffff));
-    }
-  }
-  float M = -INFINITY, zm = -INFINITY;
-  int zi = 0x7fffffff;
-#pragma unroll
-  for (int u = 0; u < MAXP; ++u) {
-    M = fmaxf(M, lo[u].z);
-    argmax_merge(zm, zi, lo[u].x, __float_as_int(lo[u].y));
-  }
-  M = block_max(M, redv);
-  block_argmax(zm, zi, redv, redi);
-  RowMerge rm;
-  rm.argmax = zi;
-  rm.M = 0.f;
-  rm.S = 1.f;
-  rm.tok = zi;
-  if (!samp) return rm;
-  float S = 0.f;
-#pragma unroll
-  for (int u = 0; u < MAXP; ++u)
-    if (lo[u].z != -INFINITY) S += lo[u].w * expf(lo[u].z - M);
-  S = block_sum(S, redv);
-  rm.M = M;
-  rm.S = S;
-  if (draw) {
-    const float lS = logf(S), lf = log_floor();
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int u = 0; u < MAXP; ++u) {
-      argmax_merge(bv, bi, hi[u].x - ((M - lo[u].z) + lS), __float_as_int(hi[u].y));
-      argmax_merge(bv, bi, lf + hi[u].z, __float_as_int(hi[u].w));
-    }
-    block_argmax(bv, bi, redv, redi);
-    rm.tok = bi;
-  }
-  return rm;
-}
-
 // Draft step i when the logits GEMM wrote the partials (one per column tile):
 // one workgroup per row.
-#define VP_WIDE_MAXP 4
 #ifndef FC_DRAFT_VP_FUSE
 #define FC_DRAFT_VP_FUSE 1
 #endif
-__global__ __launch_bounds__(VP_THR) void k_draft_finish_wide(SpecDev s, int i, const VPart* __restrict__ part,
-                                                              int nch) {
-  const int b = blockIdx.x;
-  const bool samp = s.T > 0.f;
-  const RowMerge rm = block_merge_row<VP_WIDE_MAXP>(part + (int64_t)b * nch, nch, samp, samp);
-  if (threadIdx.x == 0) {
-    s.q_stats[b * s.k + i] = make_rowstat(rm, s.V);
-    place_draft(s, b, i, rm.tok);
-  }
+#ifndef FC_DRAFT_MERGE_IN_EMBED
+#define FC_DRAFT_MERGE_IN_EMBED 1
+#endif
+__global__ __launch_bounds__(VP_THR) void k_draft_finish_wide(DraftMerge dm) { draft_merge_row(dm, blockIdx.x); }
+
+// The DraftMerge of draft step i's partials (one per column tile, nch a row)
+static DraftMerge draft_merge(const SpecDev& d, int i, const VPart* part, int nch) {
+  DraftMerge dm{};
+  dm.part = part;
+  dm.nch = nch;
+  dm.q_stats = d.q_stats;
+  dm.drafts = d.drafts;
+  dm.tok_v = d.tok_v;
+  dm.off_v = d.off_v;
+  dm.off_ds = d.off_ds;
+  dm.tok_ds = d.tok_ds;
+  dm.B = d.B;
+  dm.k = d.k;
+  dm.V = d.V;
+  dm.step = i;
+  dm.T = d.T;
+  return dm;
 }
 
 // Verify rows without top-k: merge the k+1 rows' partials into p_stats,
@@ -1698,6 +1641,7 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
   const bool fast = chunked(st);
   const PartLayout L = part_layout(st->part, B, K, V);
   const RoundChunks rcn = round_chunks(st);
+  int pend_merge = 0;  // partials per row of the previous draft step still to merge
   for (int i = 0; i < K; ++i) {
     fc_chunk ch = i == 0 ? rcn.d0 : rcn.ds;
     if (i > 0) {
@@ -1719,11 +1663,20 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
       vf.seed = st->seed;
       vf.round = st->round;
     }
+    // the previous step's partials, merged by this step's embedding kernel
+    DraftMerge dmg{};
+    if (pend_merge > 0) dmg = draft_merge(d, i - 1, L.vp, pend_merge);
     int fused = 0;
-    rc = fc_forward_vp(draft, dcache, &ch, work, work_bytes, stream, fast ? &vf : nullptr, &fused);
+    rc = fc_forward_vp(draft, dcache, &ch, work, work_bytes, stream, fast ? &vf : nullptr, &fused,
+                       pend_merge > 0 ? &dmg : nullptr);
     if (rc) return rc;
+    pend_merge = 0;
     if (fast && fused > 0) {
-      hipLaunchKernelGGL(k_draft_finish_wide, dim3(B), dim3(VP_THR), 0, s, d, i, L.vp, fused);
+      // the next draft step's chunk (one token per row) merges them in its
+      // embedding kernel; the last step's go to the verify chunk through the
+      // merge kernel
+      if (FC_DRAFT_MERGE_IN_EMBED && i + 1 < K && fc_embed_merges(draft, &rcn.ds)) pend_merge = fused;
+      else hipLaunchKernelGGL(k_draft_finish_wide, dim3(B), dim3(VP_THR), 0, s, draft_merge(d, i, L.vp, fused));
     } else if (fast) {
       int nch = 0;
       rc = launch_vpart(st->q_logits + (int64_t)i * V, (int64_t)K * V, B, V, st->temperature, st->temperature > 0.f,
