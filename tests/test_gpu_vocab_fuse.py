@@ -4,7 +4,9 @@ Without top-k, a draft step of 17-32 rows (the LDS-shared GEMM's 32 x 64
 tiles) or of 128+ rows (128 x 128 tiles) gets each logits row's argmax,
 max / exp-sum of z / T and Gumbel-max terms per column tile from the lm_head
 GEMM's epilogue, merged per row by one workgroup (flaxchat/engine.py:
-492-499: the draft's probabilities and its draw). Checked on the first
+492-499: the draft's probabilities and its draw): for steps 0..k-2 at the
+start of the next step's embedding kernel, which takes the merged draft as
+its token, for the last step by its own merge kernel. Checked on the first
 round of a bf16 session at V 65536 against the oracle: every draft is the
 oracle's draw from the device's own draft logits (oracle/sampling.py
 draft_sample, the Philox / Gumbel-max restatement), the draft and target
