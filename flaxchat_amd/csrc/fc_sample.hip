@@ -1280,6 +1280,7 @@ __global__ __launch_bounds__(VP_THR) void k_draft_finish(SpecDev s, int i, const
 #ifndef FC_DRAFT_MERGE_IN_EMBED
 #define FC_DRAFT_MERGE_IN_EMBED 1
 #endif
+static_assert(VP_THR == FC_VOCAB_THR, "the merge's workgroup size");
 __global__ __launch_bounds__(VP_THR) void k_draft_finish_wide(DraftMerge dm) { draft_merge_row(dm, blockIdx.x); }
 
 // The DraftMerge of draft step i's partials (one per column tile, nch a row)
