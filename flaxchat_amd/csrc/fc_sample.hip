@@ -1353,7 +1353,12 @@ extern "C" int32_t fc_spec_round(const fc_model* target, const fc_cache* tcache,
       rc = launch_vpart(st->q_logits + (int64_t)i * V, (int64_t)K * V, B, V, st->temperature, st->temperature > 0.f,
                         st->seed, st->round, i, L.vp, &nch, s);
       if (rc) return rc;
-      hipLaunchKernelGGL(k_draft_finish, dim3((B + 3) / 4), dim3(VP_THR), 0, s, d, i, L.vp, nch);
+      if (FC_DRAFT_MERGE_IN_EMBED && i + 1 < K && fc_embed_merges(draft, &rcn.ds) &&
+          nch <= VP_THR * VP_WIDE_MAXP) {  // the separate pass's chunks, merged the same way
+        pend_merge = nch;
+      } else {
+        hipLaunchKernelGGL(k_draft_finish, dim3((B + 3) / 4), dim3(VP_THR), 0, s, d, i, L.vp, nch);
+      }
     } else if (tk_fast(st)) {  // top-k: per-chunk candidates, then one workgroup per row
       const int nc = tk_nch(V);
       hipLaunchKernelGGL(k_topk_cand, dim3((nc + 3) / 4, B), dim3(TK_THR), 0, s, st->q_logits + (int64_t)i * V,
