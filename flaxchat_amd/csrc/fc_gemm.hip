@@ -1701,6 +1701,12 @@ struct GemmPlan {
 #ifndef FC_BIG_SPLIT
 #define FC_BIG_SPLIT 1
 #endif
+// column blocks of 64 per tile of the draft lm_head (up to 32 rows): with the
+// vocab pass in its epilogue, 32 x 128 tiles (2) measured 4.780-4.788 vs
+// 4.773-4.775 ms per cfg4 round (alternating builds)
+#ifndef FC_DRAFT_HEAD_NB
+#define FC_DRAFT_HEAD_NB 1
+#endif
 // Tile shape and K split by typical row count, from sweeps on MI355X at the
 // engine's shapes (N = 1536 / 4608 / 6144 / 65536, K = 1536 / 6144).
 static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
@@ -1746,10 +1752,10 @@ static GemmPlan plan_gemm(int Mtyp, int N, int K, int dtype, bool can_split) {
     const int wgs = std::max(1, N / 64);
     if (can_split && wgs < 256) p.S = std::min((256 + wgs - 1) / wgs, s_max);
   } else if (Mtyp <= 32) {
-    if (!can_split && N >= 16384 && N % 64 == 0) {  // draft lm_head: LDS-shared rows, 64-column tiles
+    if (!can_split && N >= 16384 && N % (64 * FC_DRAFT_HEAD_NB) == 0) {  // draft lm_head: LDS-shared rows
       p.la = true;
       p.mb = 2;
-      p.nb = 1;
+      p.nb = FC_DRAFT_HEAD_NB;  // 64-column tiles (or 128)
       return p;
     }
     p.mb = 2;
