@@ -602,7 +602,32 @@ static_assert(sizeof(Decision) == 32 * sizeof(int), "Decision layout");
 
 // mode -1: the row finished; -2: the row is stalled (it re-fed rollback
 // backlog this round and drafted nothing).
-__device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& d) {
+// The sampled acceptance test's inputs for draft position i (p and q of the
+// draft token, the uniform), which k_accept_decide's lanes load for every
+// position at once (pre != nullptr) instead of one position after another.
+struct AcceptIn {
+  float pm, pd;
+  double u;
+};
+__device__ __forceinline__ AcceptIn accept_in(const SpecDev& s, int b, const fc_rowstat* ps, int i) {
+  const int K = s.k, V = s.V;
+  // positions past the row's drafts this round hold older values; clamped so
+  // every load stays in the row (decide reads only the row's own positions)
+  const int dt = min(max(s.drafts[b * K + i], 0), V - 1);
+  const fc_rowstat qs = s.q_stats[b * K + i];
+  const float* zp = s.p_logits + ((int64_t)b * (K + 1) + i) * V;
+  const float* zq = s.q_logits + ((int64_t)b * K + i) * V;
+  AcceptIn a;
+  a.pm = prob_at(zp, ps[i], s.T, dt);
+  a.pd = prob_at(zq, qs, s.T, dt);
+  const u32x4 r = philox4x32_10(u32x4{0u, (uint32_t)b, (uint32_t)s.round[b], (uint32_t)(SLOT_ACCEPT + i)},
+                                (uint32_t)s.seed, (uint32_t)(s.seed >> 32));
+  a.u = (double)u_half(r.x);
+  return a;
+}
+
+__device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& d,
+                       const AcceptIn* pre = nullptr) {
   const int K = s.k, V = s.V;
   const bool greedy = !(s.T > 0.f);
   const int ng = s.gen_n[b] - s.prompt_len[b];
@@ -631,19 +656,14 @@ __device__ void decide(const SpecDev& s, int b, const fc_rowstat* ps, Decision& 
       ++acc;
       if (am != dt) { d.rej = i; break; }
     } else {
-      const fc_rowstat qs = s.q_stats[b * K + i];
-      const float* zp = s.p_logits + ((int64_t)b * (K + 1) + i) * V;
-      const float* zq = s.q_logits + ((int64_t)b * K + i) * V;
-      const float pm = prob_at(zp, ps[i], s.T, dt);
-      const float pd = prob_at(zq, qs, s.T, dt);
+      const AcceptIn a = pre != nullptr ? pre[i] : accept_in(s, b, ps, i);
+      const float pm = a.pm, pd = a.pd;
       if (pd == 0.f) {
         d.mode = 1; d.row = i; ++acc; d.rej = i;
         break;
       }
       const double ap = fmin(1.0, (double)pm / (double)pd);
-      const u32x4 r = philox4x32_10(u32x4{0u, (uint32_t)b, (uint32_t)s.round[b], (uint32_t)(SLOT_ACCEPT + i)},
-                                    (uint32_t)s.seed, (uint32_t)(s.seed >> 32));
-      const double u = (double)u_half(r.x);
+      const double u = a.u;
       if (u < ap) {
         d.emitted[n++] = dt;
         ++acc;
@@ -990,8 +1010,11 @@ __global__ __launch_bounds__(VP_THR) void k_accept_decide(SpecDev s, const VPart
     }
   }
   __syncthreads();
+  __shared__ AcceptIn pre[FC_PMAX];
+  if (s.T > 0.f && threadIdx.x < min(s.k, FC_PMAX)) pre[threadIdx.x] = accept_in(s, b, ps, threadIdx.x);
+  __syncthreads();
   if (threadIdx.x != 0) return;
-  decide(s, b, ps, d);
+  decide(s, b, ps, d, s.k <= FC_PMAX ? pre : nullptr);
   ctl[b] = d;
 }
 
